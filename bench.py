@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""Palettized-LUT contraction benchmark on one MI355X.
+
+Default workload (BASELINE.json metric): 4-bit palettized GEMV at batch 1,
+K=4096, N=14336 ("hero").  A step is one GEMV over one weight matrix with
+the activations already in HBM.  Steps rotate over enough distinct device
+copies of the weights (>= 2 x the 256 MB Infinity Cache) that every step
+reads its weights from HBM.  The K timed steps are captured once into a HIP
+graph and replayed, so the timed region holds K back-to-back kernels and no
+host launch cost.
+
+value = effective weight bytes (index + LUT bytes) x K / timed seconds.
+
+Other workloads (--workload): cfg1 (4-bit 4864x896), cfg2 (gate_up+SwiGLU
+2x18944x3584), cfg4 (8-bit 14336x4096, --batch B), cfg5 (prefill GEMM
+2048x4096x14336, TFLOP/s).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import platform
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+
+WORKLOADS = {
+    # name: (kind, bits, N, K, batch/M)
+    "hero": ("gemv", 4, 14336, 4096, 1),
+    "cfg1": ("gemv", 4, 4864, 896, 1),
+    "cfg2": ("gateup", 4, 18944, 3584, 1),
+    "cfg4": ("gemv", 8, 14336, 4096, 1),
+    "cfg5": ("gemm", 4, 14336, 4096, 2048),
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return platform.processor() or "unknown"
+
+
+def weight_bytes(bits: int, N: int, K: int) -> int:
+    return N * (2 << bits) + N * (K // 2 if bits == 4 else K)
+
+
+def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
+    """The oracle (a C restatement of lut_gemv_cpu, single thread like the
+    reference) timed on this host on a bounded sample of the workload."""
+    oracle = importlib.import_module("oracle")
+    oracle.lib()
+    t0 = tensors[0]
+    if kind == "gemm":
+        # M independent GEMV rows; sample rows until the budget is spent
+        rows, t_start = 0, time.perf_counter()
+        while time.perf_counter() - t_start < budget_s and rows < batch:
+            oracle.gemm(np.ascontiguousarray(x[rows:rows + 1]), t0.payload, N, K, bits, threads=1)
+            rows += 1
+        dt = time.perf_counter() - t_start
+        flops = 2.0 * rows * N * K
+        return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                "sample": f"{rows} of {batch} GEMM rows (oracle, 1 thread) in {dt:.1f} s",
+                "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+
+    def one():
+        if kind == "gateup":
+            oracle.gateup_swiglu(x[0], tensors[0].payload, tensors[1].payload, N, K, bits, threads=1)
+        else:
+            oracle.gemv(x, t0.payload, N, K, bits, threads=1)
+
+    t_start = time.perf_counter()
+    one()
+    t1 = time.perf_counter() - t_start
+    n = max(1, min(1000, int(budget_s / max(t1, 1e-6))))
+    t_start = time.perf_counter()
+    for _ in range(n):
+        one()
+    dt = (time.perf_counter() - t_start) / n
+    nbytes = weight_bytes(bits, N, K) * (2 if kind == "gateup" else 1)
+    # informational: the row-parallel variant on every host core (bit-identical)
+    threads = min(os.cpu_count() or 1, 16)
+    ts = time.perf_counter()
+    if kind == "gateup":
+        oracle.gateup_swiglu(x[0], tensors[0].payload, tensors[1].payload, N, K, bits, threads=threads)
+    else:
+        oracle.gemv(x, t0.payload, N, K, bits, threads=threads)
+    dt_mt = time.perf_counter() - ts
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n + 1} full {kind} calls of the workload (oracle, 1 thread), {dt * 1e3:.2f} ms each",
+            "all_core_value": round(nbytes / dt_mt / 1e9, 4), "all_core_threads": threads,
+            "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="hero", choices=sorted(WORKLOADS))
+    ap.add_argument("--batch", type=int, default=None, help="batch for gemv workloads (cfg4 sweep)")
+    ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes the steps rotate over")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU: the palettized contraction runs on a single "
+                                   "MI355X; multi-GPU sharding is design-only (rows per GPU + all-gather of y)",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    import torch
+    pe = importlib.import_module("prism-engine_amd")
+    kind, bits, N, K, batch = WORKLOADS[args.workload]
+    if args.batch is not None and kind == "gemv":
+        batch = args.batch
+    seed = pe.SEEDS.get(args.workload, 1000)
+
+    log(f"[bench] workload={args.workload} kind={kind} bits={bits} N={N} K={K} batch/M={batch} seed={seed}")
+    nmat = 2 if kind == "gateup" else 1
+    tensors = [pe.synth_tensor(N, K, bits, seed=seed + i) for i in range(nmat)]
+    x = pe.synth_x(batch, K, seed=seed)
+    wb = weight_bytes(bits, N, K) * nmat
+    copies = 1 if kind == "gemm" else max(2, -(-(args.rotate_mb << 20) // wb))
+
+    ctx = pe.Context(0)
+    dev = torch.device("cuda", 0)
+    weights = [[ctx.upload_tensor(t) for t in tensors] for _ in range(copies)]
+    dx = torch.from_numpy(x.view(np.int16)).to(dev)
+    ny = (batch * N) if kind != "gateup" else N
+    dy = torch.empty(ny, dtype=torch.int16, device=dev)
+    stream = torch.cuda.Stream(device=dev)
+    log(f"[bench] {copies} weight copies x {wb / 1e6:.2f} MB = {copies * wb / 1e6:.0f} MB rotated")
+
+    def launch(i: int) -> None:
+        w = weights[i % copies]
+        if kind == "gemv":
+            ctx.gemv_dev(w[0], dx, batch, dy, stream)
+        elif kind == "gateup":
+            ctx.gateup_swiglu_dev(w[0], w[1], dx, dy, stream)
+        else:
+            ctx.gemm_dev(w[0], dx, batch, dy, stream)
+
+    # correctness guard on a sample before timing (the tests hold the full bar)
+    launch(0)
+    torch.cuda.synchronize()
+    oracle = importlib.import_module("oracle")
+    yk = dy.cpu().numpy().view(np.uint16)
+    if kind == "gemv":
+        ref = oracle.gemv(x, tensors[0].payload, N, K, bits, threads=min(os.cpu_count() or 1, 16))
+        err = max(pe.rel_err(yk.reshape(batch, N)[b], ref[b]) for b in range(batch))
+    elif kind == "gateup":
+        ref = oracle.gateup_swiglu(x[0], tensors[0].payload, tensors[1].payload, N, K, bits,
+                                   threads=min(os.cpu_count() or 1, 16))
+        err = pe.rel_err(yk, ref)
+    else:
+        rows = [0, batch // 2, batch - 1]
+        ref = oracle.gemm(np.ascontiguousarray(x[rows]), tensors[0].payload, N, K, bits, threads=8)
+        err = max(pe.rel_err(yk.reshape(batch, N)[r], ref[i]) for i, r in enumerate(rows))
+    log(f"[bench] parity check rel_err={err:.3e}")
+    if not err <= 2e-3:
+        log("[bench] PARITY FAILURE")
+        return 1
+
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            launch(i)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done")
+
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(args.steps):
+                launch(i)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()  # untimed first replay (graph upload)
+        torch.cuda.synchronize()
+        log(f"[bench] captured {args.steps} launches into a HIP graph")
+
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        if graph is not None:
+            graph.replay()
+        else:
+            for i in range(args.steps):
+                launch(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = e0.elapsed_time(e1)
+    ms_step = ms / args.steps
+    log(f"[bench] timed {args.steps} steps: {ms:.3f} ms on device events, {wall * 1e3:.3f} ms wall")
+
+    if kind == "gemm":
+        flops = 2.0 * batch * N * K
+        value = flops / (ms_step * 1e-3) / 1e12
+        unit, metric = "TFLOP/s", "palettized GEMM fp16-MFMA TFLOP/s (% of 2.5 PFLOP/s dense fp16)"
+        roof = {"bound": "mfma", "achieved": round(value, 3), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(value / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": None}
+    else:
+        value = wb / (ms_step * 1e-3) / 1e9
+        unit = "GB/s"
+        metric = ("palettized GEMV effective HBM GB/s (% of 8 TB/s peak), 4-bit, batch 1"
+                  if args.workload == "hero" else
+                  f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
+        roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None}
+    kernel_name = {"gemv": "k_gemv", "gateup": "k_gemv (DUAL gate_up)", "gemm": "k_gemm"}[kind]
+    roof["kernel"] = kernel_name
+    roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        cpu = cpu_baseline(kind, bits, N, K, batch, tensors, x)
+        log(f"[bench] cpu baseline {cpu['value']} {cpu['unit']}")
+
+    rec = {
+        "metric": metric,
+        "value": round(value, 3),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4-index/fp16-LUT, fp32 accumulate" if bits == 4 else "u8-index/fp16-LUT, fp32 accumulate",
+        "data": "synthetic (seeded PCG64: x~N(0,1) fp16, uniform indices, sorted N(0,0.02) fp16 LUTs)",
+        "config": {"workload": args.workload, "kind": kind, "bits": bits, "N": N, "K": K,
+                   ("M" if kind == "gemm" else "batch"): batch, "weight_copies_rotated": copies,
+                   "launch": "hip_graph" if graph is not None else "eager", "seed": seed},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "parity_rel_err": err,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

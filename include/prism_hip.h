@@ -1,0 +1,174 @@
+/*
+ * prism_hip.h -- C ABI of the MI355X (gfx950) palettized-LUT contraction.
+ *
+ * This is the `extern "C"` layer the reference's `prism-ffi` crate would
+ * bind (prism-ffi/src/lib.rs:28-90 sets the conventions: opaque handles,
+ * constructors that return NULL on failure, `*_free` that accepts NULL,
+ * `int` results with 0 = OK and a distinct negative code per failure, -2 =
+ * backend not linked).  Plain pointers and sizes only.
+ *
+ * Weight payloads use the reference's split-block `.cimage` layout
+ * (src/lut/compiler.rs:50-61, read by compute-core/src/lut/evaluator.rs:14-31):
+ *
+ *   4-bit: [dim_m x 16 fp16 LUT, LE][dim_m x (dim_n/2) packed nibbles]
+ *          element 2i = low nibble of byte i, 2i+1 = high nibble
+ *          (src/quantization/palette.rs:207-212)
+ *   8-bit: [dim_m x 256 fp16 LUT, LE][dim_m x dim_n index bytes]
+ *          (build extension; format of compute-core/tests/
+ *           palettized_vs_direct.rs:108-135 laid out split-block)
+ *
+ * Semantics follow lut_gemv_cpu (compute-core/src/lut/evaluator.rs:21-44):
+ * fp32 accumulation, fp16 (round-to-nearest-even) output.  For 4-bit
+ * weights only the first (dim_n/8)*8 elements of a row contribute and rows
+ * are dim_n/2 bytes apart, exactly as in the reference.
+ *
+ * Thread model: a context owns one HIP stream and is not reentrant; callers
+ * serialise calls on one context (one context per thread is fine).  Entry
+ * points that take host pointers are synchronous, like
+ * MetalBackend::gemv (src/lut/engine_impl.rs:155-190).  `*_dev` entry points
+ * take device pointers and a hipStream_t (passed as void*, NULL = the
+ * context's stream) and are asynchronous.
+ */
+#ifndef PRISM_HIP_H
+#define PRISM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- result codes (compute-core/src/ffi.rs:28-43 style) ---------------- */
+#define PRISM_HIP_OK 0
+#define PRISM_HIP_ERR_NULL (-1)       /* a required pointer is NULL                 */
+#define PRISM_HIP_ERR_NOT_LINKED (-2) /* backend not linked (prism-ffi/src/lib.rs:52-56) */
+#define PRISM_HIP_ERR_SHAPE (-3)      /* dim/batch out of range or inconsistent     */
+#define PRISM_HIP_ERR_BITS (-4)       /* bits not in {4, 8}                          */
+#define PRISM_HIP_ERR_SIZE (-5)       /* payload bytes != expected for the shape     */
+#define PRISM_HIP_ERR_LAYOUT (-6)     /* unknown layout code                          */
+#define PRISM_HIP_ERR_DEVICE (-7)     /* HIP runtime error (see last_error)          */
+#define PRISM_HIP_ERR_MISMATCH (-8)   /* gate/up weights disagree in shape or bits  */
+#define PRISM_HIP_ERR_KEY (-9)        /* backend: no tensor under that key          */
+#define PRISM_HIP_ERR_CONTEXT (-10)   /* weight belongs to another context/device   */
+
+#define PRISM_HIP_LAYOUT_SPLIT_BLOCK 0u
+
+typedef struct prism_hip_ctx prism_hip_ctx;
+typedef struct prism_hip_weight prism_hip_weight;
+typedef struct prism_hip_backend prism_hip_backend;
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Replaces the device/queue half of MetalBackend::new
+ * (src/lut/engine_impl.rs:51-57,106-107): selects `device`, creates the
+ * context's stream and its staging buffers.  NULL on failure. */
+prism_hip_ctx* prism_hip_ctx_create(int device);
+void prism_hip_ctx_destroy(prism_hip_ctx* ctx); /* accepts NULL */
+
+/* Last error text of this context ("" when none).  The pointer stays valid
+ * until the next call on the context.  NULL ctx -> text of the last failed
+ * ctx_create on this thread. */
+const char* prism_hip_last_error(const prism_hip_ctx* ctx);
+
+/* Library version string (static). */
+const char* prism_hip_version(void);
+
+/* ---- weights ------------------------------------------------------------ */
+
+/* Replaces the weight upload of MetalBackend::new
+ * (src/lut/engine_impl.rs:124-133: one device copy per CompiledTensor).
+ * Copies `bytes` of host payload to device memory owned by the library.
+ * bytes must equal dim_m*2^bits*2 + dim_m*(bits==4 ? dim_n/2 : dim_n).
+ * NULL on failure (reason in prism_hip_last_error(ctx)). */
+prism_hip_weight* prism_hip_weight_upload(prism_hip_ctx* ctx, const uint8_t* payload, size_t bytes,
+                                          uint32_t dim_m, uint32_t dim_n, uint32_t bits, uint32_t layout);
+/* Same, from a payload already in device memory (copied device-to-device). */
+prism_hip_weight* prism_hip_weight_upload_dev(prism_hip_ctx* ctx, const void* d_payload, size_t bytes,
+                                              uint32_t dim_m, uint32_t dim_n, uint32_t bits, uint32_t layout);
+void prism_hip_weight_free(prism_hip_weight* w); /* accepts NULL */
+/* Shape query; any out pointer may be NULL.  Returns 0 or ERR_NULL. */
+int prism_hip_weight_info(const prism_hip_weight* w, uint32_t* dim_m, uint32_t* dim_n, uint32_t* bits,
+                          size_t* bytes);
+
+/* ---- palettized GEMV (decode) ------------------------------------------- */
+
+/* y[b, r] = f16( sum_k f32(x[b, k]) * f32(LUT_r[idx(r, k)]) ), b < batch.
+ * x: [batch x dim_n] fp16 bits, y: [batch x dim_m] fp16 bits, host memory.
+ * Replaces MetalBackend::gemv (src/lut/engine_impl.rs:155-190) and
+ * lut_gemv_cpu (compute-core/src/lut/evaluator.rs:21-44) for batch 1; a
+ * batch of B is B independent GEMVs. Synchronous. */
+int prism_hip_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t* x, uint32_t batch,
+                   uint16_t* y);
+/* Device-pointer form; asynchronous on `stream` (NULL = context stream). */
+int prism_hip_gemv_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_x, uint32_t batch,
+                       void* d_y, void* stream);
+
+/* ---- fused gate_up + SwiGLU GEMV ---------------------------------------- */
+
+/* y[r] = f16( f32(f16(silu(f32(g16[r])))) * f32(u16[r]) ) with
+ * g16 = gemv(x, gate), u16 = gemv(x, up): the CPU path's roundings
+ * (compute-core/src/lut/evaluator.rs:78-83,209-225).  Replaces
+ * MetalBackend::fused_gate_up (src/lut/engine_impl.rs:443-490) with the
+ * split-block layout and out_dim = dim_m.  x: [dim_n], y: [dim_m]. */
+int prism_hip_gateup_swiglu(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
+                            const uint16_t* x, uint16_t* y);
+int prism_hip_gateup_swiglu_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
+                                const void* d_x, void* d_y, void* stream);
+
+/* ---- palettized GEMM (prefill) ------------------------------------------ */
+
+/* Y[M x dim_m] = X[M x dim_n] . W^T, fp32 accumulation, fp16 out: M
+ * independent lut_gemv_cpu rows.  Replaces templates/palettized_gemm.metal
+ * (never dispatched by the reference; kernel_provider.rs:233-237). */
+int prism_hip_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t* X, uint32_t M, uint16_t* Y);
+int prism_hip_gemm_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
+                       void* stream);
+
+/* ---- LUT decode ---------------------------------------------------------- */
+
+/* lut_embed (compute-core/src/lut/evaluator.rs:176-197): out[0..dim_n) =
+ * fp16 bits of row `token` decoded through its LUT; token >= dim_m gives
+ * zeros.  Host memory, synchronous. */
+int prism_hip_lut_embed(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t token, uint16_t* out);
+/* Dense decode of rows [row0, row0+nrows) into d_out [nrows x dim_n] fp16
+ * (device memory, asynchronous). */
+int prism_hip_decode_rows_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, uint32_t nrows,
+                              void* d_out, void* stream);
+
+/* ---- keyed backend (MetalBackend's surface) ------------------------------ */
+
+/* A name -> weight map over one context, mirroring MetalBackend
+ * (src/lut/engine_impl.rs:31-154): `weight_bufs: HashMap<String,(Buffer,
+ * dim_m, dim_n)>`.  Errors are returned as codes; the text (the
+ * reference's `Err(String)`, e.g. "miss <key>") is in
+ * prism_hip_backend_last_error. */
+prism_hip_backend* prism_hip_backend_new(int device);
+void prism_hip_backend_free(prism_hip_backend* b); /* accepts NULL */
+const char* prism_hip_backend_last_error(const prism_hip_backend* b);
+/* Upload one CompiledTensor (src/lut/compiler.rs:14-20) under `key`;
+ * replaces an existing entry of the same key. */
+int prism_hip_backend_add_tensor(prism_hip_backend* b, const char* key, const uint8_t* payload, size_t bytes,
+                                 uint32_t dim_m, uint32_t dim_n, uint32_t bits);
+/* MetalBackend::gemv(key, inp, out) (src/lut/engine_impl.rs:155):
+ * inp_len must be dim_n (or a multiple of it: a batch), out_len dim_m
+ * times the batch. */
+int prism_hip_backend_gemv(prism_hip_backend* b, const char* key, const uint16_t* inp, size_t inp_len,
+                           uint16_t* out, size_t out_len);
+/* MetalBackend::fused_gate_up(gate_key, up_key, input, output)
+ * (src/lut/engine_impl.rs:443-449). */
+int prism_hip_backend_fused_gate_up(prism_hip_backend* b, const char* gate_key, const char* up_key,
+                                    const uint16_t* input, size_t in_len, uint16_t* output, size_t out_len);
+/* Prefill GEMM over a keyed tensor. */
+int prism_hip_backend_gemm(prism_hip_backend* b, const char* key, const uint16_t* X, uint32_t M, uint16_t* Y);
+/* The engine's embed of one token through a keyed tensor
+ * (src/lut/engine_impl.rs:1407-1446 via lut_embed). */
+int prism_hip_backend_embed(prism_hip_backend* b, const char* key, uint32_t token, uint16_t* out,
+                            size_t out_len);
+/* Number of registered tensors. */
+size_t prism_hip_backend_len(const prism_hip_backend* b);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PRISM_HIP_H */

@@ -1,0 +1,231 @@
+"""Host-side mirror of the reference's backend surface over the HIP C ABI.
+
+* :class:`Context` / :class:`Weight` wrap ``prism_hip_ctx`` /
+  ``prism_hip_weight`` (host- and device-pointer entry points).
+* :class:`HipBackend` mirrors ``MetalBackend`` (src/lut/engine_impl.rs:31-490)
+  method for method: ``new(tensors)``, ``gemv(key, inp, out)``,
+  ``fused_gate_up(gate_key, up_key, input, output)``, plus ``gemm`` and
+  ``embed``.  Where the reference returns ``Err(String)`` this raises
+  :class:`PrismHipError` with the same text ("miss <key>", ...).
+* :func:`load_cimage` uploads every palettized tensor of a `.cimage` file
+  (the weight half of ``PrismEngine::load`` + ``MetalBackend::new``,
+  engine_impl.rs:597-636,124-133).
+
+Nothing here computes on the CPU: a missing library or a device error
+raises; there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _native
+from ._native import PrismHipError, ptr
+from .palette import PalettizedTensor
+
+
+def _u16(a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    if a.dtype != np.uint16:
+        raise TypeError(f"expected fp16 bits (uint16), got {a.dtype}")
+    return a
+
+
+def _stream_handle(stream) -> int | None:
+    if stream is None:
+        return None
+    if hasattr(stream, "cuda_stream"):
+        return stream.cuda_stream
+    return int(stream)
+
+
+class Context:
+    """One device + one HIP stream (prism_hip_ctx)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _native.load()
+        self.h = self.lib.prism_hip_ctx_create(device)
+        if not self.h:
+            raise PrismHipError(_native.ERR_DEVICE, self.lib.prism_hip_last_error(None).decode())
+        self.device = device
+
+    def error(self) -> str:
+        return self.lib.prism_hip_last_error(self.h).decode()
+
+    def check(self, rc: int) -> None:
+        if rc != _native.OK:
+            raise PrismHipError(rc, self.error())
+
+    def upload(self, payload: np.ndarray, dim_m: int, dim_n: int, bits: int) -> "Weight":
+        payload = np.ascontiguousarray(payload, dtype=np.uint8)
+        h = self.lib.prism_hip_weight_upload(self.h, payload.ctypes.data, payload.size, dim_m, dim_n, bits,
+                                             _native.LAYOUT_SPLIT_BLOCK)
+        if not h:
+            raise PrismHipError(_native.ERR_SHAPE, self.error())
+        return Weight(self, h, dim_m, dim_n, bits, payload.size)
+
+    def upload_tensor(self, t: PalettizedTensor) -> "Weight":
+        return self.upload(t.payload, t.dim_m, t.dim_n, t.bits)
+
+    # -- host-pointer, synchronous
+    def gemv(self, w: "Weight", x) -> np.ndarray:
+        x = _u16(x)
+        batch = x.size // w.dim_n
+        if batch * w.dim_n != x.size:
+            raise ValueError("x size is not a multiple of dim_n")
+        y = np.empty((batch, w.dim_m), dtype=np.uint16)
+        self.check(self.lib.prism_hip_gemv(self.h, w.h, x.ctypes.data, batch, y.ctypes.data))
+        return y
+
+    def gateup_swiglu(self, gate: "Weight", up: "Weight", x) -> np.ndarray:
+        x = _u16(x)
+        y = np.empty(gate.dim_m, dtype=np.uint16)
+        self.check(self.lib.prism_hip_gateup_swiglu(self.h, gate.h, up.h, x.ctypes.data, y.ctypes.data))
+        return y
+
+    def gemm(self, w: "Weight", X) -> np.ndarray:
+        X = _u16(X)
+        M = X.size // w.dim_n
+        Y = np.empty((M, w.dim_m), dtype=np.uint16)
+        self.check(self.lib.prism_hip_gemm(self.h, w.h, X.ctypes.data, M, Y.ctypes.data))
+        return Y
+
+    def lut_embed(self, w: "Weight", token: int) -> np.ndarray:
+        out = np.empty(w.dim_n, dtype=np.uint16)
+        self.check(self.lib.prism_hip_lut_embed(self.h, w.h, token, out.ctypes.data))
+        return out
+
+    # -- device-pointer, asynchronous on `stream` (torch stream or handle)
+    def gemv_dev(self, w: "Weight", d_x, batch: int, d_y, stream=None) -> None:
+        self.check(self.lib.prism_hip_gemv_dev(self.h, w.h, ptr(d_x), batch, ptr(d_y), _stream_handle(stream)))
+
+    def gateup_swiglu_dev(self, gate: "Weight", up: "Weight", d_x, d_y, stream=None) -> None:
+        self.check(self.lib.prism_hip_gateup_swiglu_dev(self.h, gate.h, up.h, ptr(d_x), ptr(d_y),
+                                                        _stream_handle(stream)))
+
+    def gemm_dev(self, w: "Weight", d_X, M: int, d_Y, stream=None) -> None:
+        self.check(self.lib.prism_hip_gemm_dev(self.h, w.h, ptr(d_X), M, ptr(d_Y), _stream_handle(stream)))
+
+    def decode_rows_dev(self, w: "Weight", row0: int, nrows: int, d_out, stream=None) -> None:
+        self.check(self.lib.prism_hip_decode_rows_dev(self.h, w.h, row0, nrows, ptr(d_out),
+                                                      _stream_handle(stream)))
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.prism_hip_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Weight:
+    """A device copy of one palettized payload (prism_hip_weight)."""
+
+    def __init__(self, ctx: Context, h, dim_m: int, dim_n: int, bits: int, nbytes: int):
+        self.ctx, self.h = ctx, h
+        self.dim_m, self.dim_n, self.bits, self.nbytes = dim_m, dim_n, bits, nbytes
+
+    def free(self) -> None:
+        if self.h:
+            self.ctx.lib.prism_hip_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipBackend:
+    """MetalBackend's surface (src/lut/engine_impl.rs:31-490) on MI355X."""
+
+    def __init__(self, device: int = 0):
+        self.lib = _native.load()
+        self.h = self.lib.prism_hip_backend_new(device)
+        if not self.h:
+            raise PrismHipError(_native.ERR_DEVICE, self.lib.prism_hip_backend_last_error(None).decode())
+
+    @classmethod
+    def new(cls, tensors, device: int = 0) -> "HipBackend":
+        """MetalBackend::new (engine_impl.rs:51-154): uploads every tensor.
+        `tensors` maps key -> PalettizedTensor (or an iterable of them)."""
+        b = cls(device)
+        items = tensors.values() if isinstance(tensors, dict) else tensors
+        for t in items:
+            b.add_tensor(t.key, t.payload, t.dim_m, t.dim_n, t.bits)
+        return b
+
+    def _check(self, rc: int) -> None:
+        if rc != _native.OK:
+            raise PrismHipError(rc, self.lib.prism_hip_backend_last_error(self.h).decode())
+
+    def __len__(self) -> int:
+        return int(self.lib.prism_hip_backend_len(self.h))
+
+    def add_tensor(self, key: str, payload, dim_m: int, dim_n: int, bits: int = 4) -> None:
+        payload = np.ascontiguousarray(payload, dtype=np.uint8)
+        self._check(self.lib.prism_hip_backend_add_tensor(self.h, key.encode(), payload.ctypes.data, payload.size,
+                                                          dim_m, dim_n, bits))
+
+    def gemv(self, key: str, inp, out: np.ndarray | None = None, dim_m: int | None = None) -> np.ndarray:
+        """MetalBackend::gemv(key, inp, out) (engine_impl.rs:155-190)."""
+        inp = _u16(inp)
+        if out is None:
+            if dim_m is None:
+                raise ValueError("pass `out` or `dim_m`")
+            out = np.empty(dim_m * max(1, inp.size // max(1, inp.shape[-1])), dtype=np.uint16)
+        self._check(self.lib.prism_hip_backend_gemv(self.h, key.encode(), inp.ctypes.data, inp.size,
+                                                    out.ctypes.data, out.size))
+        return out
+
+    def fused_gate_up(self, gate_key: str, up_key: str, inp, out: np.ndarray) -> np.ndarray:
+        """MetalBackend::fused_gate_up (engine_impl.rs:443-490)."""
+        inp = _u16(inp)
+        self._check(self.lib.prism_hip_backend_fused_gate_up(self.h, gate_key.encode(), up_key.encode(),
+                                                             inp.ctypes.data, inp.size, out.ctypes.data,
+                                                             out.size))
+        return out
+
+    def gemm(self, key: str, X, out: np.ndarray) -> np.ndarray:
+        X = _u16(X)
+        M = out.shape[0]
+        self._check(self.lib.prism_hip_backend_gemm(self.h, key.encode(), X.ctypes.data, M, out.ctypes.data))
+        return out
+
+    def embed(self, key: str, token: int, out: np.ndarray) -> np.ndarray:
+        """lut_embed through a keyed tensor (engine_impl.rs:1407-1446)."""
+        self._check(self.lib.prism_hip_backend_embed(self.h, key.encode(), token, out.ctypes.data, out.size))
+        return out
+
+    def close(self) -> None:
+        if self.h:
+            self.lib.prism_hip_backend_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def load_cimage(path: str, device: int = 0) -> HipBackend:
+    """Upload every palettized tensor of a `.cimage` file into a HipBackend
+    (engine_impl.rs:597-636 + MetalBackend::new's upload, :124-133).  The
+    payloads are memory-mapped, not read whole."""
+    from .cimage import CImageReader, bits_of
+    b = HipBackend(device)
+    with CImageReader(path) as r:
+        for name, rec in r.tensors.items():
+            if rec["tensor_type"] not in ("Palettized4Bit", "Palettized8Bit"):
+                continue
+            b.add_tensor(name, r.payload(name), rec["dim_m"], rec["dim_n"], bits_of(rec["tensor_type"]))
+    return b

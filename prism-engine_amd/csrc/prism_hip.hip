@@ -1,0 +1,556 @@
+// prism_hip.hip -- C ABI of the MI355X palettized-LUT contraction
+// (declarations and contract: include/prism_hip.h).
+//
+// Host side: argument validation, device staging for host-pointer calls,
+// kernel selection per shape, and the keyed HipBackend that mirrors the
+// reference's MetalBackend (src/lut/engine_impl.rs:31-490).  There is no
+// CPU fallback: every failure is returned as a negative code with text.
+#include "prism_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+#include "gemm_kernels.hpp"
+#include "gemv_kernels.hpp"
+
+#define PRISM_HIP_VERSION "prism_hip 0.1 gfx950"
+
+struct prism_hip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int num_cu = 256;
+  void* d_stage = nullptr;
+  size_t stage_bytes = 0;
+  std::string err;
+};
+
+struct prism_hip_weight {
+  prism_hip_ctx* ctx = nullptr;
+  int device = 0;
+  uint32_t dim_m = 0, dim_n = 0, bits = 0, layout = 0;
+  size_t bytes = 0;
+  uint8_t* d = nullptr;
+  const uint8_t* lut() const { return d; }
+  const uint8_t* idx() const { return d + (size_t)dim_m * (2u << bits); }
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+int fail(prism_hip_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->err = buf;
+  return code;
+}
+
+#define HIP_TRY(ctx, expr)                                                                          \
+  do {                                                                                              \
+    hipError_t e_ = (expr);                                                                         \
+    if (e_ != hipSuccess)                                                                           \
+      return fail((ctx), PRISM_HIP_ERR_DEVICE, "%s failed: %s", #expr, hipGetErrorString(e_));     \
+  } while (0)
+
+size_t expected_bytes(uint32_t dm, uint32_t dn, uint32_t bits) {
+  const size_t lut = (size_t)dm * (2u << bits);
+  const size_t idx = (bits == 4) ? (size_t)dm * (dn / 2) : (size_t)dm * dn;
+  return lut + idx;
+}
+
+int check_shape(prism_hip_ctx* ctx, uint32_t dm, uint32_t dn, uint32_t bits, uint32_t layout, size_t bytes) {
+  if (bits != 4 && bits != 8) return fail(ctx, PRISM_HIP_ERR_BITS, "bits must be 4 or 8, got %u", bits);
+  if (layout != PRISM_HIP_LAYOUT_SPLIT_BLOCK) return fail(ctx, PRISM_HIP_ERR_LAYOUT, "unknown layout %u", layout);
+  if (dm == 0 || dn == 0) return fail(ctx, PRISM_HIP_ERR_SHAPE, "empty shape %ux%u", dm, dn);
+  const size_t want = expected_bytes(dm, dn, bits);
+  if (bytes != want)
+    return fail(ctx, PRISM_HIP_ERR_SIZE, "payload is %zu bytes, %u-bit %ux%u needs %zu", bytes, bits, dm, dn, want);
+  return PRISM_HIP_OK;
+}
+
+int ensure_stage(prism_hip_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->stage_bytes) return PRISM_HIP_OK;
+  if (ctx->d_stage) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipFree(ctx->d_stage));
+    ctx->d_stage = nullptr;
+    ctx->stage_bytes = 0;
+  }
+  size_t sz = 1 << 20;
+  while (sz < bytes) sz <<= 1;
+  HIP_TRY(ctx, hipMalloc(&ctx->d_stage, sz));
+  ctx->stage_bytes = sz;
+  return PRISM_HIP_OK;
+}
+
+int check_weight(prism_hip_ctx* ctx, const prism_hip_weight* w) {
+  if (!w) return fail(ctx, PRISM_HIP_ERR_NULL, "weight is NULL");
+  if (w->ctx != ctx) return fail(ctx, PRISM_HIP_ERR_CONTEXT, "weight was uploaded through another context");
+  return PRISM_HIP_OK;
+}
+
+hipStream_t pick_stream(prism_hip_ctx* ctx, void* stream) {
+  return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+// ---------------------------------------------------------------- GEMV plan
+
+struct GemvPlan {
+  const void* fn = nullptr;
+  int G = 64, CPL = 1, KW = 1, NB = 1;
+  bool fast = false;
+};
+
+template <int BITS, int NB, int CPL, bool DUAL>
+const void* gemv_fn(int G, int KW) {
+  // x slice held in VGPRs: NB * CPL * (16 or 8) registers; cap at 128.
+  if constexpr (NB * CPL * (BITS == 4 ? 16 : 8) > 128) {
+    return nullptr;
+  } else {
+#define PRISM_GK(g, kw) \
+  if (G == g && KW == kw) return reinterpret_cast<const void*>(&prism::k_gemv<BITS, NB, g, CPL, kw, DUAL>);
+    PRISM_GK(64, 1) PRISM_GK(32, 1) PRISM_GK(16, 1)
+    PRISM_GK(64, 2) PRISM_GK(16, 2)
+    PRISM_GK(64, 4) PRISM_GK(16, 4)
+#undef PRISM_GK
+    return nullptr;
+  }
+}
+
+template <int BITS, int NB, bool DUAL>
+const void* gemv_fn_cpl(int CPL, int G, int KW) {
+  switch (CPL) {
+    case 1: return gemv_fn<BITS, NB, 1, DUAL>(G, KW);
+    case 2: return gemv_fn<BITS, NB, 2, DUAL>(G, KW);
+    case 3: return gemv_fn<BITS, NB, 3, DUAL>(G, KW);
+    case 4: return gemv_fn<BITS, NB, 4, DUAL>(G, KW);
+  }
+  return nullptr;
+}
+
+const void* gemv_lookup(int bits, int NB, bool dual, int CPL, int G, int KW) {
+  if (dual) {
+    if (NB != 1) return nullptr;
+    return bits == 4 ? gemv_fn_cpl<4, 1, true>(CPL, G, KW) : gemv_fn_cpl<8, 1, true>(CPL, G, KW);
+  }
+  if (bits == 4) {
+    switch (NB) {
+      case 1: return gemv_fn_cpl<4, 1, false>(CPL, G, KW);
+      case 2: return gemv_fn_cpl<4, 2, false>(CPL, G, KW);
+      case 4: return gemv_fn_cpl<4, 4, false>(CPL, G, KW);
+      case 8: return gemv_fn_cpl<4, 8, false>(CPL, G, KW);
+    }
+  } else {
+    switch (NB) {
+      case 1: return gemv_fn_cpl<8, 1, false>(CPL, G, KW);
+      case 2: return gemv_fn_cpl<8, 2, false>(CPL, G, KW);
+      case 4: return gemv_fn_cpl<8, 4, false>(CPL, G, KW);
+      case 8: return gemv_fn_cpl<8, 8, false>(CPL, G, KW);
+    }
+  }
+  return nullptr;
+}
+
+GemvPlan plan_gemv(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
+  GemvPlan p;
+  p.NB = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
+  const uint32_t row_bytes = (bits == 4) ? K / 2 : K;
+  const bool k_ok = (bits == 4) ? (K % 32 == 0) : (K % 16 == 0);
+  if (!k_ok || (row_bytes % 16) != 0 || (xaddr % 16) != 0) return p;
+  const uint32_t C = row_bytes / 16;
+  const int xpc = (bits == 4) ? 16 : 8;
+  static const int Gs[] = {64, 32, 16};
+  static const int KWs[] = {1, 2, 4};
+  double best = 1e30;
+  for (int kw : KWs)
+    for (int g : Gs) {
+      const uint32_t lanes = (uint32_t)(kw * g);
+      const uint32_t cpl = (C + lanes - 1) / lanes;
+      if (cpl < 1 || cpl > 4) continue;
+      if ((int)cpl * p.NB * xpc > 128) continue;
+      if (dual && (int)cpl * xpc > 64) continue;
+      const void* fn = gemv_lookup((int)bits, p.NB, dual, (int)cpl, g, kw);
+      if (!fn) continue;
+      const double waste = double(lanes * cpl - C) / double(lanes * cpl);
+      // prefer: little idle lane work, then fewer waves per row (no barrier
+      // reduction), then more lanes per row (fewer LUTs per wave).
+      const double score = waste * 100.0 + (kw - 1) * 0.5 + (64 / g) * 0.01;
+      if (score < best) {
+        best = score;
+        p.fn = fn;
+        p.G = g;
+        p.CPL = (int)cpl;
+        p.KW = kw;
+        p.fast = true;
+      }
+    }
+  return p;
+}
+
+std::mutex g_occ_mu;
+std::map<std::pair<const void*, int>, int> g_occ;
+
+int occupancy(const void* fn, int threads) {
+  std::lock_guard<std::mutex> lk(g_occ_mu);
+  auto key = std::make_pair(fn, threads);
+  auto it = g_occ.find(key);
+  if (it != g_occ.end()) return it->second;
+  int nb = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, threads, 0) != hipSuccess || nb < 1) nb = 1;
+  g_occ[key] = nb;
+  return nb;
+}
+
+int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
+                uint32_t nb, void* d_y, hipStream_t st) {
+  const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
+  const bool dual = (w2 != nullptr);
+  prism::GemvArgs a;
+  a.lut = w->lut();
+  a.idx = w->idx();
+  a.lut2 = dual ? w2->lut() : nullptr;
+  a.idx2 = dual ? w2->idx() : nullptr;
+  a.N = N;
+  a.K = K;
+  for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
+    const uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
+    a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
+    a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
+    a.nb = chunk;
+    GemvPlan p = plan_gemv(bits, N, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
+    if (p.fast) {
+      const int threads = 64 * p.KW;
+      const uint32_t rpw = 64u / (uint32_t)p.G;
+      const uint32_t npass = (N + rpw - 1) / rpw;
+      const uint32_t cap = (uint32_t)ctx->num_cu * (uint32_t)occupancy(p.fn, threads);
+      const uint32_t grid = npass < cap ? npass : cap;
+      void* args[] = {&a};
+      HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(threads), args, 0, st));
+    } else {
+      const void* fn;
+      if (dual)
+        fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, true>)
+                       : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, true>);
+      else
+        fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, false>)
+                       : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, false>);
+      void* args[] = {&a};
+      HIP_TRY(ctx, hipLaunchKernel(fn, dim3(N), dim3(64), args, 0, st));
+    }
+  }
+  return PRISM_HIP_OK;
+}
+
+int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
+                hipStream_t st) {
+  const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
+  const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
+  if (!fast) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
+  const uint8_t* lut = w->lut();
+  const uint8_t* idx = w->idx();
+  const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
+  uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
+  void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K)};
+  const void* fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemm<4>)
+                             : reinterpret_cast<const void*>(&prism::k_gemm<8>);
+  HIP_TRY(ctx, hipLaunchKernel(fn, dim3(tiles), dim3(256), args, 0, st));
+  return PRISM_HIP_OK;
+}
+
+int launch_decode(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, uint32_t nrows, void* d_out,
+                  hipStream_t st) {
+  const size_t total = (size_t)nrows * w->dim_n;
+  if (total == 0) return PRISM_HIP_OK;
+  size_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  const uint8_t* lut = w->lut();
+  const uint8_t* idx = w->idx();
+  uint32_t N = w->dim_m, K = w->dim_n;
+  uint16_t* out = reinterpret_cast<uint16_t*>(d_out);
+  void* args[] = {&lut, &idx, &N, &K, &row0, &nrows, &out};
+  const void* fn = w->bits == 4 ? reinterpret_cast<const void*>(&prism::k_decode_rows<4>)
+                                : reinterpret_cast<const void*>(&prism::k_decode_rows<8>);
+  HIP_TRY(ctx, hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(256), args, 0, st));
+  return PRISM_HIP_OK;
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+}  // namespace
+
+// =========================================================================
+extern "C" {
+
+const char* prism_hip_version(void) { return PRISM_HIP_VERSION; }
+
+prism_hip_ctx* prism_hip_ctx_create(int device) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    g_create_err = std::string("no HIP device: ") + hipGetErrorString(e);
+    return nullptr;
+  }
+  if (device < 0 || device >= n) {
+    g_create_err = "device index " + std::to_string(device) + " out of range (" + std::to_string(n) + " devices)";
+    return nullptr;
+  }
+  DeviceGuard g(device);
+  hipDeviceProp_t prop;
+  if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) {
+    g_create_err = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e);
+    return nullptr;
+  }
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    g_create_err = std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950";
+    return nullptr;
+  }
+  auto* ctx = new prism_hip_ctx;
+  ctx->device = device;
+  ctx->num_cu = prop.multiProcessorCount;
+  if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
+    g_create_err = std::string("hipStreamCreate: ") + hipGetErrorString(e);
+    delete ctx;
+    return nullptr;
+  }
+  g_create_err.clear();
+  return ctx;
+}
+
+void prism_hip_ctx_destroy(prism_hip_ctx* ctx) {
+  if (!ctx) return;
+  DeviceGuard g(ctx->device);
+  if (ctx->stream) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipStreamDestroy(ctx->stream);
+  }
+  if (ctx->d_stage) (void)hipFree(ctx->d_stage);
+  delete ctx;
+}
+
+const char* prism_hip_last_error(const prism_hip_ctx* ctx) {
+  return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool src_dev, size_t bytes, uint32_t dm,
+                                     uint32_t dn, uint32_t bits, uint32_t layout) {
+  if (!ctx) return nullptr;
+  if (!src) {
+    fail(ctx, PRISM_HIP_ERR_NULL, "payload is NULL");
+    return nullptr;
+  }
+  if (check_shape(ctx, dm, dn, bits, layout, bytes) != PRISM_HIP_OK) return nullptr;
+  DeviceGuard g(ctx->device);
+  auto* w = new prism_hip_weight;
+  w->ctx = ctx;
+  w->device = ctx->device;
+  w->dim_m = dm;
+  w->dim_n = dn;
+  w->bits = bits;
+  w->layout = layout;
+  w->bytes = bytes;
+  hipError_t e = hipMalloc(&w->d, bytes);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(w->d, src, bytes, src_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload (%zu bytes): %s", bytes, hipGetErrorString(e));
+    if (w->d) (void)hipFree(w->d);
+    delete w;
+    return nullptr;
+  }
+  ctx->err.clear();
+  return w;
+}
+
+prism_hip_weight* prism_hip_weight_upload(prism_hip_ctx* ctx, const uint8_t* payload, size_t bytes, uint32_t dim_m,
+                                          uint32_t dim_n, uint32_t bits, uint32_t layout) {
+  return upload_impl(ctx, payload, false, bytes, dim_m, dim_n, bits, layout);
+}
+
+prism_hip_weight* prism_hip_weight_upload_dev(prism_hip_ctx* ctx, const void* d_payload, size_t bytes, uint32_t dim_m,
+                                              uint32_t dim_n, uint32_t bits, uint32_t layout) {
+  return upload_impl(ctx, d_payload, true, bytes, dim_m, dim_n, bits, layout);
+}
+
+void prism_hip_weight_free(prism_hip_weight* w) {
+  if (!w) return;
+  DeviceGuard g(w->device);
+  if (w->ctx && w->ctx->stream) (void)hipStreamSynchronize(w->ctx->stream);
+  if (w->d) (void)hipFree(w->d);
+  delete w;
+}
+
+int prism_hip_weight_info(const prism_hip_weight* w, uint32_t* dim_m, uint32_t* dim_n, uint32_t* bits, size_t* bytes) {
+  if (!w) return PRISM_HIP_ERR_NULL;
+  if (dim_m) *dim_m = w->dim_m;
+  if (dim_n) *dim_n = w->dim_n;
+  if (bits) *bits = w->bits;
+  if (bytes) *bytes = w->bytes;
+  return PRISM_HIP_OK;
+}
+
+// ---- GEMV
+int prism_hip_gemv_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_x, uint32_t batch, void* d_y,
+                       void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_weight(ctx, w);
+  if (rc) return rc;
+  if (!d_x || !d_y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
+  if (batch == 0) return PRISM_HIP_OK;
+  DeviceGuard g(ctx->device);
+  rc = launch_gemv(ctx, w, nullptr, d_x, batch, d_y, pick_stream(ctx, stream));
+  if (rc == PRISM_HIP_OK) ctx->err.clear();
+  return rc;
+}
+
+int prism_hip_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t* x, uint32_t batch, uint16_t* y) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_weight(ctx, w);
+  if (rc) return rc;
+  if (!x || !y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
+  if (batch == 0) return PRISM_HIP_OK;
+  DeviceGuard g(ctx->device);
+  const size_t xb = (size_t)batch * w->dim_n * 2, yb = (size_t)batch * w->dim_m * 2;
+  const size_t xoff = 0, yoff = (xb + 255) & ~(size_t)255;
+  if ((rc = ensure_stage(ctx, yoff + yb))) return rc;
+  uint8_t* st = reinterpret_cast<uint8_t*>(ctx->d_stage);
+  HIP_TRY(ctx, hipMemcpyAsync(st + xoff, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = launch_gemv(ctx, w, nullptr, st + xoff, batch, st + yoff, ctx->stream))) return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(y, st + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+// ---- gate_up + SwiGLU
+static int check_pair(prism_hip_ctx* ctx, const prism_hip_weight* g, const prism_hip_weight* u) {
+  int rc = check_weight(ctx, g);
+  if (rc) return rc;
+  if ((rc = check_weight(ctx, u))) return rc;
+  if (g->dim_m != u->dim_m || g->dim_n != u->dim_n || g->bits != u->bits)
+    return fail(ctx, PRISM_HIP_ERR_MISMATCH, "gate %ux%u/%u-bit and up %ux%u/%u-bit differ", g->dim_m, g->dim_n,
+                g->bits, u->dim_m, u->dim_n, u->bits);
+  return PRISM_HIP_OK;
+}
+
+int prism_hip_gateup_swiglu_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
+                                const void* d_x, void* d_y, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_pair(ctx, gate, up);
+  if (rc) return rc;
+  if (!d_x || !d_y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
+  DeviceGuard g(ctx->device);
+  rc = launch_gemv(ctx, gate, up, d_x, 1, d_y, pick_stream(ctx, stream));
+  if (rc == PRISM_HIP_OK) ctx->err.clear();
+  return rc;
+}
+
+int prism_hip_gateup_swiglu(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
+                            const uint16_t* x, uint16_t* y) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_pair(ctx, gate, up);
+  if (rc) return rc;
+  if (!x || !y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
+  DeviceGuard g(ctx->device);
+  const size_t xb = (size_t)gate->dim_n * 2, yb = (size_t)gate->dim_m * 2;
+  const size_t yoff = (xb + 255) & ~(size_t)255;
+  if ((rc = ensure_stage(ctx, yoff + yb))) return rc;
+  uint8_t* st = reinterpret_cast<uint8_t*>(ctx->d_stage);
+  HIP_TRY(ctx, hipMemcpyAsync(st, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = launch_gemv(ctx, gate, up, st, 1, st + yoff, ctx->stream))) return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(y, st + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+// ---- GEMM
+int prism_hip_gemm_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
+                       void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_weight(ctx, w);
+  if (rc) return rc;
+  if (!d_X || !d_Y) return fail(ctx, PRISM_HIP_ERR_NULL, "X or Y is NULL");
+  if (M == 0) return PRISM_HIP_OK;
+  DeviceGuard g(ctx->device);
+  rc = launch_gemm(ctx, w, d_X, M, d_Y, pick_stream(ctx, stream));
+  if (rc == PRISM_HIP_OK) ctx->err.clear();
+  return rc;
+}
+
+int prism_hip_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t* X, uint32_t M, uint16_t* Y) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_weight(ctx, w);
+  if (rc) return rc;
+  if (!X || !Y) return fail(ctx, PRISM_HIP_ERR_NULL, "X or Y is NULL");
+  if (M == 0) return PRISM_HIP_OK;
+  DeviceGuard g(ctx->device);
+  const size_t xb = (size_t)M * w->dim_n * 2, yb = (size_t)M * w->dim_m * 2;
+  const size_t yoff = (xb + 255) & ~(size_t)255;
+  if ((rc = ensure_stage(ctx, yoff + yb))) return rc;
+  uint8_t* st = reinterpret_cast<uint8_t*>(ctx->d_stage);
+  HIP_TRY(ctx, hipMemcpyAsync(st, X, xb, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = launch_gemm(ctx, w, st, M, st + yoff, ctx->stream))) return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(Y, st + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+// ---- decode
+int prism_hip_decode_rows_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, uint32_t nrows,
+                              void* d_out, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_weight(ctx, w);
+  if (rc) return rc;
+  if (!d_out) return fail(ctx, PRISM_HIP_ERR_NULL, "out is NULL");
+  if (row0 > w->dim_m || nrows > w->dim_m - row0)
+    return fail(ctx, PRISM_HIP_ERR_SHAPE, "rows [%u, %u) outside 0..%u", row0, row0 + nrows, w->dim_m);
+  DeviceGuard g(ctx->device);
+  rc = launch_decode(ctx, w, row0, nrows, d_out, pick_stream(ctx, stream));
+  if (rc == PRISM_HIP_OK) ctx->err.clear();
+  return rc;
+}
+
+int prism_hip_lut_embed(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t token, uint16_t* out) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_weight(ctx, w);
+  if (rc) return rc;
+  if (!out) return fail(ctx, PRISM_HIP_ERR_NULL, "out is NULL");
+  if (token >= w->dim_m) {  // evaluator.rs:182-184: out-of-range token -> zeros
+    std::memset(out, 0, (size_t)w->dim_n * 2);
+    ctx->err.clear();
+    return PRISM_HIP_OK;
+  }
+  DeviceGuard g(ctx->device);
+  const size_t ob = (size_t)w->dim_n * 2;
+  if ((rc = ensure_stage(ctx, ob))) return rc;
+  if ((rc = launch_decode(ctx, w, token, 1, ctx->d_stage, ctx->stream))) return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(out, ctx->d_stage, ob, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,241 @@
+"""HIP path vs the CPU oracle on identical seeded inputs, through the C ABI.
+
+Bar: index unpack and LUT decode bit-exact; every output vector within
+max|y - ref| / max|ref| <= 2e-3 (fp32 accumulation, fp16 output).  The GPU
+sums in a different order than the sequential CPU fold, so a few outputs
+may differ by one fp16 ulp; the tolerance is the contract.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _check(y, ref, what):
+    y = np.asarray(y).reshape(-1, np.asarray(ref).shape[-1])
+    ref = np.asarray(ref).reshape(y.shape)
+    for b in range(y.shape[0]):
+        err = _rel(y[b], ref[b])
+        assert err <= TOL, f"{what}: vector {b} rel err {err:.3e}"
+    return float(np.mean(y == ref))
+
+
+def _rel(y, ref):
+    a = y.view(np.float16).astype(np.float64)
+    r = ref.view(np.float16).astype(np.float64)
+    den = np.max(np.abs(r))
+    return float(np.max(np.abs(a - r)) / den) if den > 0 else float(np.max(np.abs(a)))
+
+
+# (bits, N, K): BASELINE shapes, decode-step shapes and ragged edges
+GEMV_SHAPES = [
+    (4, 4864, 896),      # config 1
+    (4, 14336, 4096),    # hero
+    (4, 18944, 3584),    # config 2 matrix
+    (4, 896, 4864),      # Qwen down_proj
+    (4, 128, 896),       # Qwen k/v proj
+    (4, 1, 32), (4, 3, 64), (4, 17, 96), (4, 65, 160), (4, 100, 2080),
+    (4, 5, 8), (4, 9, 24), (4, 7, 40), (4, 6, 100), (4, 4, 12), (4, 3, 4),  # ragged K: generic path
+    (8, 14336, 4096),    # config 4
+    (8, 1, 16), (8, 31, 48), (8, 64, 4096), (8, 9, 7), (8, 3, 100),
+]
+
+
+@pytest.mark.parametrize("bits,N,K", GEMV_SHAPES)
+def test_gemv_b1(pe, oracle, gpu_ctx, bits, N, K):
+    t = pe.synth_tensor(N, K, bits, seed=N * 7 + K)
+    x = pe.synth_x(1, K, seed=N + K)
+    w = gpu_ctx.upload_tensor(t)
+    y = gpu_ctx.gemv(w, x)
+    ref = oracle.gemv(x, t.payload, N, K, bits, threads=8)
+    exact = _check(y, ref, f"{bits}-bit {N}x{K}")
+    assert exact > 0.95
+    w.free()
+
+
+@pytest.mark.parametrize("bits,N,K", [(8, 14336, 4096), (4, 14336, 4096), (8, 300, 512), (4, 300, 896)])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 11])
+def test_gemv_batch(pe, oracle, gpu_ctx, bits, N, K, batch):
+    if N * K > 10**7 and batch in (3, 11):
+        pytest.skip("odd batches covered at the smaller shapes")
+    t = pe.synth_tensor(N, K, bits, seed=batch + bits)
+    x = pe.synth_x(batch, K, seed=batch)
+    w = gpu_ctx.upload_tensor(t)
+    y = gpu_ctx.gemv(w, x)
+    ref = oracle.gemv(x, t.payload, N, K, bits, threads=8)
+    _check(y, ref, f"{bits}-bit batch {batch}")
+    w.free()
+
+
+@pytest.mark.parametrize("bits,N,K", [(4, 4864, 896), (4, 1000, 4096), (8, 700, 4096), (4, 33, 40), (8, 20, 24)])
+def test_decode_bit_exact_through_gemv(pe, gpu_ctx, bits, N, K):
+    """One-hot x (x = e_k) makes every output the decoded weight itself:
+    y[r] = LUT_r[idx(r, k)] exactly, through the GEMV kernel's own decode."""
+    t = pe.synth_tensor(N, K, bits, seed=K + 3)
+    lut, idx = pe.unpack_payload(t.payload, N, K, bits)
+    keff = (K // 8) * 8 if bits == 4 else K
+    ks = sorted(set([0, 1, keff - 1, keff // 2, 7 % keff, (keff * 5) // 8]))
+    x = np.zeros((len(ks), K), dtype=np.float16)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    w = gpu_ctx.upload_tensor(t)
+    y = gpu_ctx.gemv(w, x.view(np.uint16))
+    for i, k in enumerate(ks):
+        want = lut[np.arange(N), idx[:, k]]
+        want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
+        assert np.array_equal(y[i], want), f"column {k}"
+    w.free()
+
+
+@pytest.mark.parametrize("bits,N,K", [(4, 4864, 896), (8, 300, 4096), (4, 7, 100), (8, 5, 33)])
+def test_decode_rows_bit_exact(pe, oracle, gpu_ctx, bits, N, K):
+    import torch
+    t = pe.synth_tensor(N, K, bits, seed=N)
+    w = gpu_ctx.upload_tensor(t)
+    out = torch.empty((N, K), dtype=torch.int16, device="cuda")
+    gpu_ctx.decode_rows_dev(w, 0, N, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, oracle.decode_rows(t.payload, N, K, bits))
+    for tok in (0, N // 2, N - 1, N, N + 5):
+        e = gpu_ctx.lut_embed(w, tok)
+        assert np.array_equal(e, oracle.decode_rows(t.payload, N, K, bits, tok, 1)[0] if tok < N
+                              else np.zeros(K, np.uint16))
+    if bits == 4:
+        assert np.array_equal(gpu_ctx.lut_embed(w, 1), oracle.lut_embed(1, t.payload, N, K))
+    w.free()
+
+
+@pytest.mark.parametrize("bits,N,K", [(4, 18944, 3584), (4, 4864, 896), (4, 50, 128), (4, 9, 40), (8, 700, 1024)])
+def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
+    g = pe.synth_tensor(N, K, bits, seed=2 * N + 1)
+    u = pe.synth_tensor(N, K, bits, seed=2 * N + 2)
+    x = pe.synth_x(1, K, seed=K)
+    wg, wu = gpu_ctx.upload_tensor(g), gpu_ctx.upload_tensor(u)
+    y = gpu_ctx.gateup_swiglu(wg, wu, x)
+    ref = oracle.gateup_swiglu(x[0], g.payload, u.payload, N, K, bits, threads=8)
+    _check(y, ref, f"gate_up {N}x{K}")
+    wg.free()
+    wu.free()
+
+
+@pytest.mark.parametrize("bits,M,N,K", [(4, 64, 256, 512), (4, 77, 200, 96), (8, 40, 130, 256),
+                                        (4, 3, 5, 64), (4, 10, 20, 40), (4, 300, 1000, 1024)])
+def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
+    t = pe.synth_tensor(N, K, bits, seed=M + N)
+    X = pe.synth_x(M, K, seed=M)
+    w = gpu_ctx.upload_tensor(t)
+    Y = gpu_ctx.gemm(w, X)
+    ref = oracle.gemm(X, t.payload, N, K, bits, threads=8)
+    _check(Y, ref, f"gemm {M}x{N}x{K}")
+    w.free()
+
+
+def test_gemm_config5_sampled(pe, oracle, gpu_ctx):
+    """Config 5 at full size (X 2048x4096, W 14336x4096 4-bit): 24 sampled
+    rows against the oracle, and every row against a float32 BLAS product of
+    the dequantized W (second oracle)."""
+    import torch
+    M, N, K = 2048, 14336, 4096
+    t = pe.synth_tensor(N, K, 4, seed=pe.SEEDS["cfg5"])
+    X = pe.synth_x(M, K, seed=pe.SEEDS["cfg5"])
+    w = gpu_ctx.upload_tensor(t)
+    dX = torch.from_numpy(X.view(np.int16)).cuda()
+    dY = torch.empty((M, N), dtype=torch.int16, device="cuda")
+    gpu_ctx.gemm_dev(w, dX, M, dY)
+    torch.cuda.synchronize()
+    Y = dY.cpu().numpy().view(np.uint16)
+    rows = np.random.default_rng(0).choice(M, 24, replace=False)
+    ref = oracle.gemm(np.ascontiguousarray(X[rows]), t.payload, N, K, 4, threads=8)
+    _check(Y[rows], ref, "gemm cfg5 sampled rows")
+    Wd = torch.from_numpy(pe.dequantize(t.payload, N, K, 4))
+    Xf = torch.from_numpy(X.view(np.float16).astype(np.float32))
+    R = (Xf[:256] @ Wd.T).numpy()
+    Yf = Y[:256].view(np.float16).astype(np.float32)
+    den = np.max(np.abs(R), axis=1)
+    assert np.all(np.max(np.abs(Yf - R), axis=1) / den <= TOL)
+    w.free()
+
+
+def test_errors_never_crash(pe, gpu_ctx):
+    lib = gpu_ctx.lib
+    t = pe.synth_tensor(16, 64, 4, seed=1)
+    p = t.payload
+    assert lib.prism_hip_weight_upload(gpu_ctx.h, p.ctypes.data, p.size, 16, 64, 5, 0) is None
+    assert "bits" in gpu_ctx.error()
+    assert lib.prism_hip_weight_upload(gpu_ctx.h, p.ctypes.data, p.size - 1, 16, 64, 4, 0) is None
+    assert "needs" in gpu_ctx.error()
+    assert lib.prism_hip_weight_upload(gpu_ctx.h, p.ctypes.data, p.size, 16, 64, 4, 3) is None
+    assert lib.prism_hip_weight_upload(gpu_ctx.h, p.ctypes.data, 0, 0, 64, 4, 0) is None
+    w = gpu_ctx.upload_tensor(t)
+    u = gpu_ctx.upload_tensor(pe.synth_tensor(16, 32, 4, seed=2))
+    x = pe.synth_x(1, 64, seed=1)
+    y = np.zeros(16, np.uint16)
+    assert lib.prism_hip_gateup_swiglu(gpu_ctx.h, w.h, u.h, x.ctypes.data, y.ctypes.data) == -8
+    assert lib.prism_hip_gemv(gpu_ctx.h, w.h, None, 1, y.ctypes.data) == -1
+    assert lib.prism_hip_gemv(gpu_ctx.h, None, x.ctypes.data, 1, y.ctypes.data) == -1
+    other = pe.Context(0)
+    assert lib.prism_hip_gemv(other.h, w.h, x.ctypes.data, 1, y.ctypes.data) == -10
+    other.close()
+    assert lib.prism_hip_gemv(gpu_ctx.h, w.h, x.ctypes.data, 0, y.ctypes.data) == 0  # empty batch
+    import torch
+    d = torch.empty(16 * 64, dtype=torch.int16, device="cuda")
+    assert lib.prism_hip_decode_rows_dev(gpu_ctx.h, w.h, 10, 7, d.data_ptr(), None) == -3
+    w.free()
+    u.free()
+
+
+def test_backend_keyed_surface(pe, oracle):
+    """HipBackend mirrors MetalBackend: keyed gemv / fused_gate_up, "miss
+    <key>" on an unknown tensor, embed of an out-of-range token is zeros."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    q = pe.synth_tensor(896, 896, 4, seed=1, key="layers.0.q_proj")
+    g = pe.synth_tensor(4864, 896, 4, seed=2, key="layers.0.gate_proj")
+    u = pe.synth_tensor(4864, 896, 4, seed=3, key="layers.0.up_proj")
+    b = pe.HipBackend.new({t.key: t for t in (q, g, u)})
+    assert len(b) == 3
+    x = pe.synth_x(1, 896, seed=4)[0]
+    out = np.zeros(896, np.uint16)
+    b.gemv("layers.0.q_proj", x, out)
+    _check(out, oracle.lut_gemv4(x, q.payload, 896, 896), "backend gemv")
+    with pytest.raises(pe.PrismHipError, match="miss nope"):
+        b.gemv("nope", x, out)
+    with pytest.raises(pe.PrismHipError):
+        b.gemv("layers.0.q_proj", x[:100], out)
+    y = np.zeros(4864, np.uint16)
+    b.fused_gate_up("layers.0.gate_proj", "layers.0.up_proj", x, y)
+    _check(y, oracle.gateup_swiglu(x, g.payload, u.payload, 4864, 896), "backend fused_gate_up")
+    with pytest.raises(pe.PrismHipError, match="miss layers.0.nope"):
+        b.fused_gate_up("layers.0.gate_proj", "layers.0.nope", x, y)
+    e = np.ones(896, np.uint16)
+    b.embed("layers.0.q_proj", 5000, e)
+    assert np.all(e == 0)
+    b.embed("layers.0.q_proj", 3, e)
+    assert np.array_equal(e, oracle.lut_embed(3, q.payload, 896, 896))
+    b.close()
+
+
+def test_cimage_load_to_backend(pe, oracle, tmp_path):
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    path = str(tmp_path / "m.cimage")
+    wr = pe.CImageWriter(path)
+    ts = [pe.synth_tensor(256, 512, 4, seed=i, key=f"layers.{i}.o_proj") for i in range(3)]
+    for t in ts:
+        wr.append_palettized(t.key, t.payload, t.dim_m, t.dim_n)
+    t8 = pe.synth_tensor(128, 256, 8, seed=9, key="w8")
+    wr.append_palettized("w8", t8.payload, 128, 256, bits=8)
+    wr.finalize()
+    b = pe.load_cimage(path)
+    assert len(b) == 4
+    x = pe.synth_x(1, 512, seed=5)[0]
+    for t in ts:
+        out = np.zeros(256, np.uint16)
+        b.gemv(t.key, x, out)
+        _check(out, oracle.lut_gemv4(x, t.payload, 256, 512), t.key)
+    b.close()

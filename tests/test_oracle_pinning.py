@@ -1,0 +1,200 @@
+"""Pins the CPU oracle (oracle/prism_cpuref.c) before anything trusts it.
+
+Each check is independent of the oracle's own code: the reference's known
+answers, numpy's IEEE binary16 conversions, numpy's sequential float32
+cumsum, float64 bounds and closed forms -- chosen so that a dropped term, a
+swapped nibble, a wrong LUT offset or row stride, or a wrong rounding fails.
+"""
+import numpy as np
+import pytest
+
+
+# ---------------------------------------------------------------- f16 <-> f32
+
+def test_f16_to_f32_exhaustive(oracle):
+    """All 65536 binary16 patterns against numpy's exact widening."""
+    L = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([L.cpuref_f16_to_f32(int(b)) for b in bits], dtype=np.float32)
+    finite = np.isfinite(ref)
+    assert np.array_equal(got[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+
+
+def test_f32_to_f16_rne(oracle):
+    """Round-to-nearest-even narrowing vs numpy on edge cases and random values
+    spanning normal, subnormal, overflow and tie cases."""
+    L = oracle.lib()
+    rng = np.random.default_rng(0)
+    special = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e9, -1e9, 6.1035156e-05,
+                        5.9604645e-08, 2.9802322e-08, 2.9802326e-08, 8.940697e-08, 1e-45, np.inf, -np.inf,
+                        1.0009765625, 1.00048828125, 1.00146484375, 2049.0, 2051.0, -3.0517578e-05],
+                       dtype=np.float32)
+    rand = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32),
+        (rng.standard_normal(100000) * 1e-5).astype(np.float32),
+        (rng.standard_normal(100000) * 3e4).astype(np.float32),
+        rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+    ])
+    vals = np.concatenate([special, rand])
+    vals = vals[~np.isnan(vals)]
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([L.cpuref_f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, ref)
+    nan = L.cpuref_f32_to_f16(float("nan"))
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x03FF) != 0
+
+
+# ---------------------------------------------------------------- reference KATs
+
+def test_kat_lut_gemv(oracle):
+    """compute-core/src/lut/evaluator.rs:231-246: 2x8 matrix, row-0 LUT all
+    1.0, indices 0, x = 1.0 -> o[0] ~= 8.0 (exactly 8.0 in fp16)."""
+    p = bytearray()
+    for _ in range(16):
+        p += (0x3C00).to_bytes(2, "little")
+    for _ in range(16):
+        p += (0x4000).to_bytes(2, "little")
+    p += bytes(8)
+    p = np.frombuffer(bytes(p), dtype=np.uint8).copy()
+    o = oracle.lut_gemv4(np.full(8, 0x3C00, dtype=np.uint16), p, 2, 8)
+    assert abs(float(o.view(np.float16)[0]) - 8.0) < 0.01
+    assert o[0] == 0x4800  # 8.0
+    assert o[1] == 0x4C00  # row 1: LUT all 2.0 -> 16.0
+
+
+def test_kat_lut_embed(oracle):
+    """evaluator.rs:267-284: LUT decode returns the LUT bits; an out-of-range
+    token gives zeros."""
+    payload = np.frombuffer(b"".join((0x3C00).to_bytes(2, "little") for _ in range(32)) + bytes(8),
+                            dtype=np.uint8).copy()
+    v = oracle.lut_embed(0, payload, 2, 8)
+    assert v.size == 8 and np.all(v == 0x3C00)
+    assert np.all(oracle.lut_embed(5, payload, 2, 8) == 0)
+
+
+def test_kat_silu_gate_up(oracle):
+    """evaluator.rs:286-298: silu(2)*3 ~= 5.2848 within 0.01."""
+    g = np.full(4, np.float16(2.0)).view(np.uint16)
+    u = np.full(4, np.float16(3.0)).view(np.uint16)
+    out = oracle.swiglu(g, u).view(np.float16).astype(np.float32)
+    expected = np.float32(2.0) / (np.float32(1.0) + np.exp(np.float32(-2.0)))
+    assert np.all(np.abs(out - expected * 3) < 0.01)
+
+
+def test_kat_nibble_order(pe, oracle):
+    """palette.rs:410-425: [1,2,3,4] with LUT [1,2,3,4,0...] packs to
+    [0x10, 0x32]; the oracle's decode of that payload gives the values back."""
+    packed, mse = pe.encode_channel(np.array([1.0, 2.0, 3.0, 4.0]), np.array([1, 2, 3, 4] + [0] * 12, dtype=float))
+    assert list(packed) == [0x10, 0x32] and mse < 1e-3
+    lut = np.array([1, 2, 3, 4] + [0] * 12, dtype=np.float16)
+    payload = np.concatenate([lut.view(np.uint8), packed]).astype(np.uint8)
+    # K=4 is below one 8-element word: lut_gemv_cpu drops it (evaluator.rs:33).
+    assert np.all(oracle.decode_rows(payload, 1, 4, 4) == 0)
+    payload8 = np.concatenate([lut.view(np.uint8), packed, np.array([0x54, 0x76], dtype=np.uint8)])
+    dec = oracle.decode_rows(payload8.astype(np.uint8), 1, 8, 4)[0].view(np.float16)
+    assert list(dec[:4]) == [1, 2, 3, 4]
+
+
+# ---------------------------------------------------------------- independent restatement via numpy
+
+def _numpy_seq(x_bits, payload, dm, dn, bits, pe):
+    """Sequential fp32 fold via numpy's float32 cumsum (a library routine,
+    sequential by definition) over numpy-unpacked weights."""
+    w = pe.dequantize(payload, dm, dn, bits)  # fp32, 4-bit tail zeroed
+    keff = (dn // 8) * 8 if bits == 4 else dn
+    x = np.asarray(x_bits).view(np.float16).astype(np.float32)[:keff]
+    prods = (w[:, :keff] * x[None, :]).astype(np.float32)
+    if keff == 0:
+        return np.zeros(dm, dtype=np.float16).view(np.uint16)
+    acc = np.cumsum(prods, axis=1, dtype=np.float32)[:, -1]
+    return acc.astype(np.float16).view(np.uint16)
+
+
+@pytest.mark.parametrize("bits,dm,dn", [(4, 7, 8), (4, 33, 64), (4, 64, 128), (4, 5, 12), (4, 3, 100),
+                                        (4, 16, 896), (8, 7, 8), (8, 33, 50), (8, 64, 128), (8, 4, 1)])
+def test_oracle_matches_numpy_fold(pe, oracle, bits, dm, dn):
+    t = pe.synth_tensor(dm, dn, bits, seed=dm * 131 + dn)
+    x = pe.synth_x(1, dn, seed=dm + dn)[0]
+    got = oracle.gemv(x, t.payload, dm, dn, bits)[0]
+    ref = _numpy_seq(x, t.payload, dm, dn, bits, pe)
+    assert np.array_equal(got, ref)
+
+
+def test_oracle_float64_bound(pe, oracle):
+    """|y32 - y64| <= gamma_K * sum|x w| + half an fp16 ulp of the result."""
+    dm, dn = 128, 4096
+    t = pe.synth_tensor(dm, dn, 4, seed=3)
+    x = pe.synth_x(1, dn, seed=3)[0]
+    y = oracle.lut_gemv4(x, t.payload, dm, dn).view(np.float16).astype(np.float64)
+    w = pe.dequantize(t.payload, dm, dn, 4).astype(np.float64)
+    xf = x.view(np.float16).astype(np.float64)
+    y64 = w @ xf
+    gamma = dn * 2.0 ** -24 / (1 - dn * 2.0 ** -24)
+    bound = gamma * (np.abs(w) @ np.abs(xf)) + np.abs(y64) * 2.0 ** -11 + 2.0 ** -25
+    assert np.all(np.abs(y - y64) <= bound * 1.0001)
+
+
+def test_oracle_closed_forms(pe, oracle):
+    """Constant LUT c gives f16(c * sum x) exactly when every partial sum is
+    exact (x = small integers, c = power of two); one-hot x returns the
+    selected LUT entry bit for bit; a wrong nibble order or row stride fails."""
+    dm, dn = 9, 64
+    rng = np.random.default_rng(5)
+    idx = rng.integers(0, 16, size=(dm, dn), dtype=np.uint8)
+    lut = np.full((dm, 16), np.float16(0.25))
+    payload = pe.split_block_payload(lut, idx, 4)
+    xi = rng.integers(-3, 4, size=dn).astype(np.float16)
+    y = oracle.lut_gemv4(xi.view(np.uint16), payload, dm, dn).view(np.float16)
+    assert np.all(y == np.float16(0.25 * float(xi.astype(np.float64).sum())))
+    # one-hot: distinct LUTs per row
+    lut = rng.standard_normal((dm, 16)).astype(np.float16)
+    payload = pe.split_block_payload(lut, idx, 4)
+    for k in (0, 1, 2, 7, 8, 31, 62, 63):
+        x = np.zeros(dn, dtype=np.float16)
+        x[k] = 1.0
+        y = oracle.lut_gemv4(x.view(np.uint16), payload, dm, dn)
+        want = lut[np.arange(dm), idx[:, k]].view(np.uint16)
+        want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
+        assert np.array_equal(y, want), k
+
+
+def test_oracle_batch_and_gemm_rows(pe, oracle):
+    """A batch of B and a GEMM of M rows are B / M independent GEMVs."""
+    dm, dn = 40, 96
+    for bits in (4, 8):
+        t = pe.synth_tensor(dm, dn, bits, seed=11 + bits)
+        X = pe.synth_x(5, dn, seed=bits)
+        Yb = oracle.gemv(X, t.payload, dm, dn, bits)
+        Yg = oracle.gemm(X, t.payload, dm, dn, bits, threads=2)
+        assert np.array_equal(Yb, Yg)
+        for b in range(5):
+            assert np.array_equal(Yb[b], _numpy_seq(X[b], t.payload, dm, dn, bits, pe))
+
+
+def test_oracle_gateup_composition(pe, oracle):
+    """gate_up+SwiGLU = two GEMVs, silu with the f16 rounding, f16(g*u),
+    against a numpy float32 restatement of evaluator.rs:78-83,209-225."""
+    dm, dn = 64, 256
+    g = pe.synth_tensor(dm, dn, 4, seed=21)
+    u = pe.synth_tensor(dm, dn, 4, seed=22)
+    x = pe.synth_x(1, dn, seed=23)[0]
+    y = oracle.gateup_swiglu(x, g.payload, u.payload, dm, dn)
+    g16 = _numpy_seq(x, g.payload, dm, dn, 4, pe).view(np.float16).astype(np.float32)
+    u16 = _numpy_seq(x, u.payload, dm, dn, 4, pe).view(np.float16).astype(np.float32)
+    s = (g16 / (np.float32(1) + np.exp(-g16))).astype(np.float16).astype(np.float32)
+    ref = (s * u16).astype(np.float16).view(np.uint16)
+    # expf of glibc vs numpy's exp may differ in the last f32 bit; after the
+    # fp16 roundings the outputs agree except on exact ties.
+    assert np.mean(y == ref) > 0.99
+    assert pe.rel_err(y, ref) <= 2e-3
+
+
+def test_oracle_threads_bit_identical(pe, oracle):
+    t = pe.synth_tensor(300, 512, 4, seed=9)
+    x = pe.synth_x(1, 512, seed=9)[0]
+    assert np.array_equal(oracle.lut_gemv4(x, t.payload, 300, 512),
+                          oracle.lut_gemv4(x, t.payload, 300, 512, threads=4))
