@@ -16,7 +16,7 @@ raises; there is no fallback path.
 """
 from __future__ import annotations
 
-import ctypes
+import sys
 
 import numpy as np
 
@@ -119,6 +119,9 @@ class Context:
             self.h = None
 
     def __del__(self):
+        # no HIP calls while the interpreter tears down (the runtime may be gone)
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -138,6 +141,8 @@ class Weight:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.free()
         except Exception:
@@ -211,6 +216,8 @@ class HipBackend:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:

@@ -16,8 +16,10 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 
 #include "gemm_kernels.hpp"
+#include "gemv_fast.hpp"
 #include "gemv_kernels.hpp"
 
 #define PRISM_HIP_VERSION "prism_hip 0.1 gfx950"
@@ -29,6 +31,9 @@ struct prism_hip_ctx {
   void* d_stage = nullptr;
   size_t stage_bytes = 0;
   std::string err;
+  // Weights uploaded through this context; destroying the context orphans
+  // them (w->ctx = nullptr) so a later prism_hip_weight_free stays valid.
+  std::unordered_set<prism_hip_weight*> weights;
 };
 
 struct prism_hip_weight {
@@ -211,6 +216,72 @@ int occupancy(const void* fn, int threads) {
   return nb;
 }
 
+// ---- wave-per-row-block kernel (gemv_fast.hpp)
+struct WavePlan {
+  const void* fn = nullptr;
+  int PR = 1;
+  size_t lds = 0;
+};
+
+template <int BITS, int CPL, int PR, bool DUAL, int NB>
+WavePlan wave_entry() {
+  WavePlan w;
+  w.fn = reinterpret_cast<const void*>(&prism::k_gemv_wave<BITS, CPL, PR, DUAL, NB>);
+  w.PR = PR;
+  w.lds = prism::gemv_wave_lds_bytes<BITS, CPL, PR, DUAL, NB>();
+  return w;
+}
+
+template <int BITS, int CPL, bool DUAL, int NB>
+WavePlan wave_pick_pr(int pr) {
+  if constexpr (NB * CPL * (BITS == 4 ? 16 : 8) > 128) {
+    return WavePlan{};
+  } else {
+    (void)pr;  // two rows per wave measured best for the 4096/3584-wide shapes
+    return wave_entry<BITS, CPL, 2, DUAL, NB>();
+  }
+}
+
+template <int BITS, bool DUAL, int NB>
+WavePlan wave_pick_cpl(int cpl, int pr) {
+  switch (cpl) {
+    case 1: return wave_pick_pr<BITS, 1, DUAL, NB>(pr);
+    case 2: return wave_pick_pr<BITS, 2, DUAL, NB>(pr);
+    case 3: return wave_pick_pr<BITS, 3, DUAL, NB>(pr);
+    case 4: return wave_pick_pr<BITS, 4, DUAL, NB>(pr);
+  }
+  return WavePlan{};
+}
+
+// Use the wave kernel when a row is at least 48 16-byte chunks and the last
+// lane pass is >= 75% full; returns fn == nullptr otherwise.
+WavePlan plan_wave(uint32_t bits, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
+  const uint32_t row_bytes = (bits == 4) ? K / 2 : K;
+  const bool k_ok = (bits == 4) ? (K % 32 == 0) : (K % 16 == 0);
+  if (!k_ok || row_bytes % 16 != 0 || xaddr % 16 != 0) return WavePlan{};
+  const uint32_t C = row_bytes / 16;
+  const uint32_t cpl = (C + 63) / 64;
+  if (C < 48 || cpl > 4 || C * 4 < cpl * 64 * 3) return WavePlan{};
+  const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : 4;
+  const int pr = 2;
+  if (dual) {
+    if (nb != 1) return WavePlan{};
+    return bits == 4 ? wave_pick_cpl<4, true, 1>((int)cpl, pr) : wave_pick_cpl<8, true, 1>((int)cpl, pr);
+  }
+  if (bits == 4) {
+    switch (NB) {
+      case 1: return wave_pick_cpl<4, false, 1>((int)cpl, pr);
+      case 2: return wave_pick_cpl<4, false, 2>((int)cpl, pr);
+      default: return wave_pick_cpl<4, false, 4>((int)cpl, pr);
+    }
+  }
+  switch (NB) {
+    case 1: return wave_pick_cpl<8, false, 1>((int)cpl, pr);
+    case 2: return wave_pick_cpl<8, false, 2>((int)cpl, pr);
+    default: return wave_pick_cpl<8, false, 4>((int)cpl, pr);
+  }
+}
+
 int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
                 uint32_t nb, void* d_y, hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
@@ -222,6 +293,24 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
   a.idx2 = dual ? w2->idx() : nullptr;
   a.N = N;
   a.K = K;
+  // batches of <= 4 vectors go to the wave kernel when the shape suits it
+  {
+    const uint32_t step = 4;
+    WavePlan wp = plan_wave(bits, K, nb < step ? nb : step, dual, reinterpret_cast<uintptr_t>(d_x));
+    if (wp.fn && ((size_t)K * 2) % 16 == 0) {
+      for (uint32_t b0 = 0; b0 < nb; b0 += step) {
+        const uint32_t chunk = (nb - b0 < step) ? nb - b0 : step;
+        a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
+        a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
+        a.nb = chunk;
+        WavePlan p = plan_wave(bits, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
+        const uint32_t grid = (N + (uint32_t)p.PR - 1) / (uint32_t)p.PR;
+        void* args[] = {&a};
+        HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(64), args, p.lds, st));
+      }
+      return PRISM_HIP_OK;
+    }
+  }
   for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
     const uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
@@ -340,6 +429,8 @@ prism_hip_ctx* prism_hip_ctx_create(int device) {
 void prism_hip_ctx_destroy(prism_hip_ctx* ctx) {
   if (!ctx) return;
   DeviceGuard g(ctx->device);
+  for (prism_hip_weight* w : ctx->weights) w->ctx = nullptr;
+  ctx->weights.clear();
   if (ctx->stream) {
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamDestroy(ctx->stream);
@@ -379,6 +470,7 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
     delete w;
     return nullptr;
   }
+  ctx->weights.insert(w);
   ctx->err.clear();
   return w;
 }
@@ -396,8 +488,8 @@ prism_hip_weight* prism_hip_weight_upload_dev(prism_hip_ctx* ctx, const void* d_
 void prism_hip_weight_free(prism_hip_weight* w) {
   if (!w) return;
   DeviceGuard g(w->device);
-  if (w->ctx && w->ctx->stream) (void)hipStreamSynchronize(w->ctx->stream);
-  if (w->d) (void)hipFree(w->d);
+  if (w->ctx) w->ctx->weights.erase(w);
+  if (w->d) (void)hipFree(w->d);  // hipFree waits for work still using the buffer
   delete w;
 }
 
