@@ -121,6 +121,9 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes the steps rotate over")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="after timing, run one untimed device copy of MB MiB (scale reference for "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -218,6 +221,15 @@ def main() -> int:
     ms = e0.elapsed_time(e1)
     ms_step = ms / args.steps
     log(f"[bench] timed {args.steps} steps: {ms:.3f} ms on device events, {wall * 1e3:.3f} ms wall")
+
+    if args.copy_calibration > 0:
+        src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: {args.copy_calibration} MiB device-to-device copy done")
+        del src, dst
 
     if kind == "gemm":
         flops = 2.0 * batch * N * K
