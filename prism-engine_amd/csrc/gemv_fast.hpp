@@ -19,9 +19,10 @@
 //    fp16 pair that v_dot2_f32_f16 multiplies with the matching x pair:
 //    1 VALU op + 1/2 LDS read per element.  Measured on MI355X, random
 //    reads over 256 dwords run at ~13 lanes/clk/CU against ~29 for a
-//    conflict-free 16-entry table, but the halved read count and the
-//    dropped packing op make the pair table faster end to end (7.6 vs
-//    8.9 us for the 4096 x 14336 matrix);
+//    conflict-free 16-entry table; with the halved read count and no
+//    packing op the two decodes time the same on the 4096 x 14336 matrix
+//    (8.8-8.9 us, random indices), and the pair table needs fewer VGPRs
+//    (69 vs 96), so every wave of the grid is resident at once;
 //  * 8-bit: the 256-entry LUT itself is the table; each byte costs one SDWA
 //    shift and one ds_read_u16, and pairs are packed with v_lshl_or_b32;
 //  * x (the lane's fixed 32*CPL-element slice) is loaded once into VGPRs;
