@@ -181,4 +181,234 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ lut, c
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_gemm_w4: 4-bit prefill GEMM that decodes W straight into MFMA B-operand
+// registers (no decoded-W tile in LDS).
+//
+// * Block tile 256 (M) x 256 (N), 4 waves (one per SIMD); wave w owns all
+//   256 M rows and N columns [64w, +64): 8 x 2 tiles of
+//   v_mfma_f32_32x32x16_f16, 256 fp32 accumulators per lane (AGPRs).  Each
+//   decoded B operand feeds 8 MFMAs and each A fragment 2, which keeps the
+//   VALU decode at ~40 % and the LDS fragment reads at ~50 % of the MFMA
+//   time; the step loop is software-pipelined (next step's B decoded while
+//   the current step's MFMAs run) and interleaved with
+//   sched_group_barrier so one wave per SIMD keeps the matrix core fed.
+// * B operand (weights): lane (j = lane%32, h = lane/32) of N-subtile t
+//   always holds weight row n0 + 64w + 32t + j, so it keeps that row's LUT
+//   in 8 VGPRs as byte planes (lo / hi bytes of entries 0-3, 4-7, 8-11,
+//   12-15) for the whole K loop.  One index dword (8 nibbles) is decoded
+//   with v_perm_b32 byte selects (two 8-byte windows and a bit-3 v_bfi
+//   merge for lo and hi bytes, then two interleaving perms): 25 VALU ops
+//   for the 4 VGPRs of one MFMA B operand, which co-issue under the 8
+//   MFMAs (8 M-subtiles) that consume it.
+// * The decoded halves come out in k order (0,2,4,6,1,3,5,7) of the
+//   dword's 8 nibbles; the X tile is stored in LDS with every group of 8
+//   halves permuted the same way, so A (X) and B agree on k.
+// * X tile (A operand) 256 x 64 fp16 in LDS, double-buffered, 144-byte row
+//   pitch (16-byte fragment reads of 8 consecutive rows hit 32 distinct
+//   banks); the next K step's X tile and index chunks are loaded from global
+//   memory while the current step's MFMAs run; one barrier per K step.
+// * Per 64-wide K step a lane loads 16 index bytes of each of its two rows
+//   (bytes [32*it + 16h, +16), i.e. nibbles [64*it + 32h, +32)); MFMA step
+//   q in {0..3} uses dword q, so lane half h covers k = 64*it + 32h + 8q +
+//   {0,2,4,6,1,3,5,7}.
+// Requires K % 64 == 0.
+struct LutPlanes {
+  uint32_t l0, l1, l2, l3, h0, h1, h2, h3;
+};
+
+__device__ __forceinline__ uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) { return (a & m) | (b & ~m); }
+
+__device__ __forceinline__ LutPlanes make_planes(const uint4 ra, const uint4 rb) {
+  // ra = LUT dwords 0..3 (entries 0..7), rb = dwords 4..7 (entries 8..15)
+  LutPlanes P;
+  P.l0 = __builtin_amdgcn_perm(ra.y, ra.x, 0x06040200u);
+  P.h0 = __builtin_amdgcn_perm(ra.y, ra.x, 0x07050301u);
+  P.l1 = __builtin_amdgcn_perm(ra.w, ra.z, 0x06040200u);
+  P.h1 = __builtin_amdgcn_perm(ra.w, ra.z, 0x07050301u);
+  P.l2 = __builtin_amdgcn_perm(rb.y, rb.x, 0x06040200u);
+  P.h2 = __builtin_amdgcn_perm(rb.y, rb.x, 0x07050301u);
+  P.l3 = __builtin_amdgcn_perm(rb.w, rb.z, 0x06040200u);
+  P.h3 = __builtin_amdgcn_perm(rb.w, rb.z, 0x07050301u);
+  return P;
+}
+
+// 8 nibbles -> 8 fp16 in k order (0,2,4,6,1,3,5,7) as an MFMA operand.
+__device__ __forceinline__ half8_t decode_nib8(uint32_t w, const LutPlanes& P) {
+  const uint32_t se = w & 0x07070707u;
+  const uint32_t so = (w >> 4) & 0x07070707u;
+  const uint32_t me = __builtin_amdgcn_perm(0xFFFFFFFFu, 0u, (w >> 1) & 0x07070707u);
+  const uint32_t mo = __builtin_amdgcn_perm(0xFFFFFFFFu, 0u, (w >> 5) & 0x07070707u);
+  const uint32_t le = bsel(me, __builtin_amdgcn_perm(P.l3, P.l2, se), __builtin_amdgcn_perm(P.l1, P.l0, se));
+  const uint32_t he = bsel(me, __builtin_amdgcn_perm(P.h3, P.h2, se), __builtin_amdgcn_perm(P.h1, P.h0, se));
+  const uint32_t lo = bsel(mo, __builtin_amdgcn_perm(P.l3, P.l2, so), __builtin_amdgcn_perm(P.l1, P.l0, so));
+  const uint32_t ho = bsel(mo, __builtin_amdgcn_perm(P.h3, P.h2, so), __builtin_amdgcn_perm(P.h1, P.h0, so));
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  u32x4v v;
+  v.x = __builtin_amdgcn_perm(he, le, 0x05010400u);
+  v.y = __builtin_amdgcn_perm(he, le, 0x07030602u);
+  v.z = __builtin_amdgcn_perm(ho, lo, 0x05010400u);
+  v.w = __builtin_amdgcn_perm(ho, lo, 0x07030602u);
+  return __builtin_bit_cast(half8_t, v);
+}
+
+constexpr int GW4_BM = 256;
+constexpr int GW4_BN = 256;
+constexpr int GW4_BK = 64;
+constexpr int GW4_PITCH = GW4_BK + 8;  // halves per LDS row (144 B)
+
+__global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
+                                                 const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
+                                                 uint32_t N, uint32_t K) {
+  constexpr int BM = GW4_BM, BN = GW4_BN, BK = GW4_BK, P = GW4_PITCH;
+  __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * P];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;  // wave tile: all 256 M rows, N cols [64*wave, +64)
+  const int j = lane & 31, h = lane >> 5;
+
+  const uint32_t mt = (M + BM - 1) / BM;
+  const uint32_t nt = (N + BN - 1) / BN;
+  const uint32_t ntiles = mt * nt;
+  uint32_t t = blockIdx.x;
+  {
+    // XCD-aware: block b runs on XCD b % 8; XCD x takes a contiguous tile
+    // range, N-fastest, so its W rows and X rows stay in its own L2.
+    const uint32_t per = ntiles / 8, rem = ntiles % 8;
+    const uint32_t xcd = t % 8, slot = t / 8;
+    const uint32_t start = xcd * per + (xcd < rem ? xcd : rem);
+    t = start + slot;
+  }
+  const uint32_t n0 = (t % nt) * BN;
+  const uint32_t m0 = (t / nt) * BM;
+  const uint32_t row_bytes = K / 2;
+  const uint32_t nk = K / BK;
+
+  // ---- this lane's two weight rows: LUT planes and index row pointers
+  LutPlanes pl[2];
+  const uint8_t* wrow[2];
+#pragma unroll
+  for (int s = 0; s < 2; s++) {
+    uint32_t n = n0 + 64 * wave + 32 * s + j;
+    n = n < N ? n : N - 1;
+    const uint4* lr = reinterpret_cast<const uint4*>(lut + (size_t)n * 32);
+    pl[s] = make_planes(lr[0], lr[1]);
+    wrow[s] = idx + (size_t)n * row_bytes + 16 * h;
+  }
+
+  // ---- X tile loads: 256 rows x 128 B = 2048 chunks of 16 B, 8 per thread
+  uint4 xs[8];
+  auto load_x = [&](uint32_t it) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int c = tid + 256 * i;
+      uint32_t m = m0 + (c >> 3);
+      m = m < M ? m : M - 1;
+      xs[i] = *reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)it * BK + 8 * (c & 7));
+    }
+  };
+  // permute each group of 8 halves to k order (0,2,4,6,1,3,5,7) and store
+  auto store_x = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int c = tid + 256 * i;
+      const uint4 v = xs[i];
+      uint4 o;
+      o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
+      o.y = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
+      o.z = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
+      o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
+      *reinterpret_cast<uint4*>(&sX[buf][(c >> 3) * P + 8 * (c & 7)]) = o;
+    }
+  };
+  uint4 wc[2], wn2[2];
+  auto load_w = [&](uint32_t it, uint4 (&dst)[2]) {
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      dst[s] = *reinterpret_cast<const uint4*>(wrow[s] + (size_t)it * 32);
+      // opaque to the optimizer: keep the loaded words in registers instead
+      // of re-issuing the (read-only) load next to a later use
+      asm volatile("" : "+v"(dst[s].x), "+v"(dst[s].y), "+v"(dst[s].z), "+v"(dst[s].w));
+    }
+  };
+  auto wdword = [](const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; };
+
+  floatx16 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][s][e] = 0.0f;
+
+  load_x(0);
+  load_w(0, wc);
+  store_x(0);
+  __syncthreads();
+  // Software pipeline over MFMA steps: the B operands of the next step are
+  // decoded while the current step's 16 MFMAs run (two register sets,
+  // indexed by step parity); A fragments are read next to their MFMAs.
+  half8_t bop[2][2];
+  bop[0][0] = decode_nib8(wc[0].x, pl[0]);
+  bop[0][1] = decode_nib8(wc[1].x, pl[1]);
+  int buf = 0;
+  for (uint32_t it = 0; it < nk; it++) {
+    // next K block's global loads (clamped on the last block: a re-read of
+    // the same tile, L2 hits) -- keeps the loop body one straight-line block
+    const uint32_t itn = it + 1 < nk ? it + 1 : it;
+    load_x(itn);
+    load_w(itn, wn2);
+    const uint16_t* xb = &sX[buf][j * P + 32 * h];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int cur = q & 1, nxt = cur ^ 1;
+      half8_t a[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) a[i] = *reinterpret_cast<const half8_t*>(xb + 32 * i * P + 8 * q);
+      if (q < 3) {
+        bop[nxt][0] = decode_nib8(wdword(wc[0], q + 1), pl[0]);
+        bop[nxt][1] = decode_nib8(wdword(wc[1], q + 1), pl[1]);
+      } else {
+        bop[nxt][0] = decode_nib8(wn2[0].x, pl[0]);
+        bop[nxt][1] = decode_nib8(wn2[1].x, pl[1]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bop[cur][0], acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bop[cur][1], acc[i][1], 0, 0, 0);
+      }
+      // interleave: per MFMA pair, one A fragment read and ~3 VALU ops each
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      }
+    }
+    store_x(buf ^ 1);
+    wc[0] = wn2[0];
+    wc[1] = wn2[1];
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // ---- epilogue: D lane layout: col j = lane%32, row 8*(e/4) + 4*(lane/32) + e%4
+  const bool full = (m0 + BM <= M) && (n0 + BN <= N);
+#pragma unroll
+  for (int s = 0; s < 2; s++) {
+    const uint32_t n = n0 + 64 * wave + 32 * s + j;
+    uint16_t* yc = Y + n;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const uint32_t m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
+        if (full || (m < M && n < N)) yc[(size_t)m * N] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][s][e]);
+      }
+  }
+}
+
 }  // namespace prism

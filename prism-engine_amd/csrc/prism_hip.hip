@@ -345,6 +345,19 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
   if (!fast) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  if (bits == 4 && K % prism::GW4_BK == 0) {
+    // register-decode MFMA kernel (gemm_kernels.hpp, k_gemm_w4)
+    const uint32_t tiles4 =
+        ((M + prism::GW4_BM - 1) / prism::GW4_BM) * ((N + prism::GW4_BN - 1) / prism::GW4_BN);
+    const uint8_t* lut = w->lut();
+    const uint8_t* idx = w->idx();
+    const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
+    uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
+    void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K)};
+    HIP_TRY(ctx, hipLaunchKernel(reinterpret_cast<const void*>(&prism::k_gemm_w4), dim3(tiles4), dim3(256), args, 0,
+                                 st));
+    return PRISM_HIP_OK;
+  }
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
   const uint8_t* lut = w->lut();
   const uint8_t* idx = w->idx();
