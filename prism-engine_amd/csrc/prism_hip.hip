@@ -293,8 +293,9 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
   a.idx2 = dual ? w2->idx() : nullptr;
   a.N = N;
   a.K = K;
-  // batches of <= 4 vectors go to the wave kernel when the shape suits it
-  {
+  // batches of <= 4 vectors go to the wave kernel when the shape suits it;
+  // larger batches use k_gemv (up to 8 vectors per pass over the weights)
+  if (nb <= 4) {
     const uint32_t step = 4;
     WavePlan wp = plan_wave(bits, K, nb < step ? nb : step, dual, reinterpret_cast<uintptr_t>(d_x));
     if (wp.fn && ((size_t)K * 2) % 16 == 0) {
