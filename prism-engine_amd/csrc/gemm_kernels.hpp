@@ -22,9 +22,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lut_perm.hpp"
+
 namespace prism {
 
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int GEMM_BM = 128;
@@ -213,45 +214,6 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ lut, c
 //   q in {0..3} uses dword q, so lane half h covers k = 64*it + 32h + 8q +
 //   {0,2,4,6,1,3,5,7}.
 // Requires K % 64 == 0.
-struct LutPlanes {
-  uint32_t l0, l1, l2, l3, h0, h1, h2, h3;
-};
-
-__device__ __forceinline__ uint32_t bsel(uint32_t m, uint32_t a, uint32_t b) { return (a & m) | (b & ~m); }
-
-__device__ __forceinline__ LutPlanes make_planes(const uint4 ra, const uint4 rb) {
-  // ra = LUT dwords 0..3 (entries 0..7), rb = dwords 4..7 (entries 8..15)
-  LutPlanes P;
-  P.l0 = __builtin_amdgcn_perm(ra.y, ra.x, 0x06040200u);
-  P.h0 = __builtin_amdgcn_perm(ra.y, ra.x, 0x07050301u);
-  P.l1 = __builtin_amdgcn_perm(ra.w, ra.z, 0x06040200u);
-  P.h1 = __builtin_amdgcn_perm(ra.w, ra.z, 0x07050301u);
-  P.l2 = __builtin_amdgcn_perm(rb.y, rb.x, 0x06040200u);
-  P.h2 = __builtin_amdgcn_perm(rb.y, rb.x, 0x07050301u);
-  P.l3 = __builtin_amdgcn_perm(rb.w, rb.z, 0x06040200u);
-  P.h3 = __builtin_amdgcn_perm(rb.w, rb.z, 0x07050301u);
-  return P;
-}
-
-// 8 nibbles -> 8 fp16 in k order (0,2,4,6,1,3,5,7) as an MFMA operand.
-__device__ __forceinline__ half8_t decode_nib8(uint32_t w, const LutPlanes& P) {
-  const uint32_t se = w & 0x07070707u;
-  const uint32_t so = (w >> 4) & 0x07070707u;
-  const uint32_t me = __builtin_amdgcn_perm(0xFFFFFFFFu, 0u, (w >> 1) & 0x07070707u);
-  const uint32_t mo = __builtin_amdgcn_perm(0xFFFFFFFFu, 0u, (w >> 5) & 0x07070707u);
-  const uint32_t le = bsel(me, __builtin_amdgcn_perm(P.l3, P.l2, se), __builtin_amdgcn_perm(P.l1, P.l0, se));
-  const uint32_t he = bsel(me, __builtin_amdgcn_perm(P.h3, P.h2, se), __builtin_amdgcn_perm(P.h1, P.h0, se));
-  const uint32_t lo = bsel(mo, __builtin_amdgcn_perm(P.l3, P.l2, so), __builtin_amdgcn_perm(P.l1, P.l0, so));
-  const uint32_t ho = bsel(mo, __builtin_amdgcn_perm(P.h3, P.h2, so), __builtin_amdgcn_perm(P.h1, P.h0, so));
-  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-  u32x4v v;
-  v.x = __builtin_amdgcn_perm(he, le, 0x05010400u);
-  v.y = __builtin_amdgcn_perm(he, le, 0x07030602u);
-  v.z = __builtin_amdgcn_perm(ho, lo, 0x05010400u);
-  v.w = __builtin_amdgcn_perm(ho, lo, 0x07030602u);
-  return __builtin_bit_cast(half8_t, v);
-}
-
 constexpr int GW4_BM = 256;
 constexpr int GW4_BN = 256;
 constexpr int GW4_BK = 64;

@@ -12,15 +12,13 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
-#include <map>
-#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
 
 #include "gemm_kernels.hpp"
-#include "gemv_fast.hpp"
 #include "gemv_kernels.hpp"
+#include "gemv_tile.hpp"
 
 #define PRISM_HIP_VERSION "prism_hip 0.1 gfx950"
 
@@ -109,176 +107,74 @@ hipStream_t pick_stream(prism_hip_ctx* ctx, void* stream) {
 }
 
 // ---------------------------------------------------------------- GEMV plan
+// k_gemv_tile (gemv_tile.hpp) for K % 8 == 0 with 16-byte aligned x, in
+// passes of up to 8 batch vectors; k_gemv_generic otherwise.
 
-struct GemvPlan {
+struct TilePlan {
   const void* fn = nullptr;
-  int G = 64, CPL = 1, KW = 1, NB = 1;
-  bool fast = false;
-};
-
-template <int BITS, int NB, int CPL, bool DUAL>
-const void* gemv_fn(int G, int KW) {
-  // x slice held in VGPRs: NB * CPL * (16 or 8) registers; cap at 128.
-  if constexpr (NB * CPL * (BITS == 4 ? 16 : 8) > 128) {
-    return nullptr;
-  } else {
-#define PRISM_GK(g, kw) \
-  if (G == g && KW == kw) return reinterpret_cast<const void*>(&prism::k_gemv<BITS, NB, g, CPL, kw, DUAL>);
-    PRISM_GK(64, 1) PRISM_GK(32, 1) PRISM_GK(16, 1)
-    PRISM_GK(64, 2) PRISM_GK(16, 2)
-    PRISM_GK(64, 4) PRISM_GK(16, 4)
-#undef PRISM_GK
-    return nullptr;
-  }
-}
-
-template <int BITS, int NB, bool DUAL>
-const void* gemv_fn_cpl(int CPL, int G, int KW) {
-  switch (CPL) {
-    case 1: return gemv_fn<BITS, NB, 1, DUAL>(G, KW);
-    case 2: return gemv_fn<BITS, NB, 2, DUAL>(G, KW);
-    case 3: return gemv_fn<BITS, NB, 3, DUAL>(G, KW);
-    case 4: return gemv_fn<BITS, NB, 4, DUAL>(G, KW);
-  }
-  return nullptr;
-}
-
-const void* gemv_lookup(int bits, int NB, bool dual, int CPL, int G, int KW) {
-  if (dual) {
-    if (NB != 1) return nullptr;
-    return bits == 4 ? gemv_fn_cpl<4, 1, true>(CPL, G, KW) : gemv_fn_cpl<8, 1, true>(CPL, G, KW);
-  }
-  if (bits == 4) {
-    switch (NB) {
-      case 1: return gemv_fn_cpl<4, 1, false>(CPL, G, KW);
-      case 2: return gemv_fn_cpl<4, 2, false>(CPL, G, KW);
-      case 4: return gemv_fn_cpl<4, 4, false>(CPL, G, KW);
-      case 8: return gemv_fn_cpl<4, 8, false>(CPL, G, KW);
-    }
-  } else {
-    switch (NB) {
-      case 1: return gemv_fn_cpl<8, 1, false>(CPL, G, KW);
-      case 2: return gemv_fn_cpl<8, 2, false>(CPL, G, KW);
-      case 4: return gemv_fn_cpl<8, 4, false>(CPL, G, KW);
-      case 8: return gemv_fn_cpl<8, 8, false>(CPL, G, KW);
-    }
-  }
-  return nullptr;
-}
-
-GemvPlan plan_gemv(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
-  GemvPlan p;
-  p.NB = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
-  const uint32_t row_bytes = (bits == 4) ? K / 2 : K;
-  const bool k_ok = (bits == 4) ? (K % 32 == 0) : (K % 16 == 0);
-  if (!k_ok || (row_bytes % 16) != 0 || (xaddr % 16) != 0) return p;
-  const uint32_t C = row_bytes / 16;
-  const int xpc = (bits == 4) ? 16 : 8;
-  static const int Gs[] = {64, 32, 16};
-  static const int KWs[] = {1, 2, 4};
-  double best = 1e30;
-  for (int kw : KWs)
-    for (int g : Gs) {
-      const uint32_t lanes = (uint32_t)(kw * g);
-      const uint32_t cpl = (C + lanes - 1) / lanes;
-      if (cpl < 1 || cpl > 4) continue;
-      if ((int)cpl * p.NB * xpc > 128) continue;
-      if (dual && (int)cpl * xpc > 64) continue;
-      const void* fn = gemv_lookup((int)bits, p.NB, dual, (int)cpl, g, kw);
-      if (!fn) continue;
-      const double waste = double(lanes * cpl - C) / double(lanes * cpl);
-      // prefer: little idle lane work, then fewer waves per row (no barrier
-      // reduction), then more lanes per row (fewer LUTs per wave).
-      const double score = waste * 100.0 + (kw - 1) * 0.5 + (64 / g) * 0.01;
-      if (score < best) {
-        best = score;
-        p.fn = fn;
-        p.G = g;
-        p.CPL = (int)cpl;
-        p.KW = kw;
-        p.fast = true;
-      }
-    }
-  return p;
-}
-
-std::mutex g_occ_mu;
-std::map<std::pair<const void*, int>, int> g_occ;
-
-int occupancy(const void* fn, int threads) {
-  std::lock_guard<std::mutex> lk(g_occ_mu);
-  auto key = std::make_pair(fn, threads);
-  auto it = g_occ.find(key);
-  if (it != g_occ.end()) return it->second;
-  int nb = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, threads, 0) != hipSuccess || nb < 1) nb = 1;
-  g_occ[key] = nb;
-  return nb;
-}
-
-// ---- wave-per-row-block kernel (gemv_fast.hpp)
-struct WavePlan {
-  const void* fn = nullptr;
-  int PR = 1;
+  int threads = 0;
+  int R = 1;
   size_t lds = 0;
 };
 
-template <int BITS, int CPL, int PR, bool DUAL, int NB>
-WavePlan wave_entry() {
-  WavePlan w;
-  w.fn = reinterpret_cast<const void*>(&prism::k_gemv_wave<BITS, CPL, PR, DUAL, NB>);
-  w.PR = PR;
-  w.lds = prism::gemv_wave_lds_bytes<BITS, CPL, PR, DUAL, NB>();
-  return w;
+template <int BITS, int UPL, int R, bool DUAL, int NB>
+TilePlan tile_entry(int threads) {
+  TilePlan p;
+  p.fn = reinterpret_cast<const void*>(&prism::k_gemv_tile<BITS, UPL, R, DUAL, NB>);
+  p.threads = threads;
+  p.R = R;
+  p.lds = prism::gemv_tile_lds_bytes<BITS, R, DUAL, NB>(threads);
+  return p;
 }
 
-template <int BITS, int CPL, bool DUAL, int NB>
-WavePlan wave_pick_pr(int pr) {
-  if constexpr (NB * CPL * (BITS == 4 ? 16 : 8) > 128) {
-    return WavePlan{};
-  } else {
-    (void)pr;  // two rows per wave measured best for the 4096/3584-wide shapes
-    return wave_entry<BITS, CPL, 2, DUAL, NB>();
+// x units held in VGPRs: NB * UPL * 4 registers, at most 64.
+template <int BITS, int R, bool DUAL, int NB>
+TilePlan tile_pick_upl(int upl, int threads) {
+  switch (upl) {
+#define PRISM_TU(u) \
+  case u:           \
+    if constexpr (NB * (u) <= 16) return tile_entry<BITS, u, R, DUAL, NB>(threads); else return TilePlan{};
+    PRISM_TU(1) PRISM_TU(2) PRISM_TU(3) PRISM_TU(4) PRISM_TU(5) PRISM_TU(6) PRISM_TU(7) PRISM_TU(8)
+#undef PRISM_TU
   }
+  return TilePlan{};
 }
 
-template <int BITS, bool DUAL, int NB>
-WavePlan wave_pick_cpl(int cpl, int pr) {
-  switch (cpl) {
-    case 1: return wave_pick_pr<BITS, 1, DUAL, NB>(pr);
-    case 2: return wave_pick_pr<BITS, 2, DUAL, NB>(pr);
-    case 3: return wave_pick_pr<BITS, 3, DUAL, NB>(pr);
-    case 4: return wave_pick_pr<BITS, 4, DUAL, NB>(pr);
-  }
-  return WavePlan{};
-}
-
-// Use the wave kernel when a row is at least 48 16-byte chunks and the last
-// lane pass is >= 75% full; returns fn == nullptr otherwise.
-WavePlan plan_wave(uint32_t bits, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
-  const uint32_t row_bytes = (bits == 4) ? K / 2 : K;
-  const bool k_ok = (bits == 4) ? (K % 32 == 0) : (K % 16 == 0);
-  if (!k_ok || row_bytes % 16 != 0 || xaddr % 16 != 0) return WavePlan{};
-  const uint32_t C = row_bytes / 16;
-  const uint32_t cpl = (C + 63) / 64;
-  if (C < 48 || cpl > 4 || C * 4 < cpl * 64 * 3) return WavePlan{};
-  const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : 4;
-  const int pr = 2;
-  if (dual) {
-    if (nb != 1) return WavePlan{};
-    return bits == 4 ? wave_pick_cpl<4, true, 1>((int)cpl, pr) : wave_pick_cpl<8, true, 1>((int)cpl, pr);
-  }
+// Rows per workgroup: 2 (4 tables for gate+up), 4 for 4+ batch vectors and
+// for 8-bit weights (whose LUT loads are spread over >= 256 threads).
+TilePlan plan_tile(uint32_t bits, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
+  if (K % 8 != 0 || K == 0 || xaddr % 16 != 0) return TilePlan{};
+  const uint32_t U = K / 8;
+  const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
+  if (dual && NB != 1) return TilePlan{};
+  const uint32_t uplmax = (uint32_t)(16 / NB < 8 ? 16 / NB : 8);
+  // waves per workgroup: the fewest that keep UPL <= uplmax; 4-bit rows of
+  // 65..128 units (K <= 1024) use 2 waves, 8-bit ones at least 4
+  uint32_t W = 0;
+  const uint32_t wmin = bits == 8 ? 4u : (U > 64 && U <= 128 && NB == 1) ? 2u : 1u;
+  for (uint32_t w = wmin; w <= 8; w *= 2)
+    if ((U + 64 * w - 1) / (64 * w) <= uplmax) {
+      W = w;
+      break;
+    }
+  if (!W) return TilePlan{};
+  const int upl = (int)((U + 64 * W - 1) / (64 * W));
+  const int threads = (int)(64 * W);
   if (bits == 4) {
+    if (dual) return tile_pick_upl<4, 2, true, 1>(upl, threads);
     switch (NB) {
-      case 1: return wave_pick_cpl<4, false, 1>((int)cpl, pr);
-      case 2: return wave_pick_cpl<4, false, 2>((int)cpl, pr);
-      default: return wave_pick_cpl<4, false, 4>((int)cpl, pr);
+      case 1: return tile_pick_upl<4, 2, false, 1>(upl, threads);
+      case 2: return tile_pick_upl<4, 2, false, 2>(upl, threads);
+      case 4: return tile_pick_upl<4, 4, false, 4>(upl, threads);
+      default: return tile_pick_upl<4, 4, false, 8>(upl, threads);
     }
   }
+  if (dual) return tile_pick_upl<8, 2, true, 1>(upl, threads);
   switch (NB) {
-    case 1: return wave_pick_cpl<8, false, 1>((int)cpl, pr);
-    case 2: return wave_pick_cpl<8, false, 2>((int)cpl, pr);
-    default: return wave_pick_cpl<8, false, 4>((int)cpl, pr);
+    case 1: return tile_pick_upl<8, 4, false, 1>(upl, threads);
+    case 2: return tile_pick_upl<8, 4, false, 2>(upl, threads);
+    case 4: return tile_pick_upl<8, 4, false, 4>(upl, threads);
+    default: return tile_pick_upl<8, 4, false, 8>(upl, threads);
   }
 }
 
@@ -293,39 +189,16 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
   a.idx2 = dual ? w2->idx() : nullptr;
   a.N = N;
   a.K = K;
-  // batches of <= 4 vectors go to the wave kernel when the shape suits it;
-  // larger batches use k_gemv (up to 8 vectors per pass over the weights)
-  if (nb <= 4) {
-    const uint32_t step = 4;
-    WavePlan wp = plan_wave(bits, K, nb < step ? nb : step, dual, reinterpret_cast<uintptr_t>(d_x));
-    if (wp.fn && ((size_t)K * 2) % 16 == 0) {
-      for (uint32_t b0 = 0; b0 < nb; b0 += step) {
-        const uint32_t chunk = (nb - b0 < step) ? nb - b0 : step;
-        a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
-        a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
-        a.nb = chunk;
-        WavePlan p = plan_wave(bits, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
-        const uint32_t grid = (N + (uint32_t)p.PR - 1) / (uint32_t)p.PR;
-        void* args[] = {&a};
-        HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(64), args, p.lds, st));
-      }
-      return PRISM_HIP_OK;
-    }
-  }
   for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
     const uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
     a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
     a.nb = chunk;
-    GemvPlan p = plan_gemv(bits, N, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
-    if (p.fast) {
-      const int threads = 64 * p.KW;
-      const uint32_t rpw = 64u / (uint32_t)p.G;
-      const uint32_t npass = (N + rpw - 1) / rpw;
-      const uint32_t cap = (uint32_t)ctx->num_cu * (uint32_t)occupancy(p.fn, threads);
-      const uint32_t grid = npass < cap ? npass : cap;
-      void* args[] = {&a};
-      HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(threads), args, 0, st));
+    const TilePlan p = plan_tile(bits, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
+    void* args[] = {&a};
+    if (p.fn) {
+      const uint32_t grid = (N + (uint32_t)p.R - 1) / (uint32_t)p.R;
+      HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(p.threads), args, p.lds, st));
     } else {
       const void* fn;
       if (dual)
@@ -334,7 +207,6 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
       else
         fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, false>)
                        : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, false>);
-      void* args[] = {&a};
       HIP_TRY(ctx, hipLaunchKernel(fn, dim3(N), dim3(64), args, 0, st));
     }
   }
