@@ -15,9 +15,10 @@
 //    workgroups read the same x, so its re-reads land on a few L2 channels;
 //    keeping them well below the streamed index bytes matters;
 //  * the LUT dwords, the x units and every index unit of the R rows are
-//    issued up front (straight-line code, clamped addresses), so the
-//    compiler counts them with vmcnt and each row is decoded as soon as its
-//    bytes land;
+//    issued up front (straight-line code), so the compiler counts them with
+//    vmcnt and each row is decoded as soon as its bytes land; x and index
+//    loads are buffer loads (one lane offset, the unit step as an
+//    immediate, range checking instead of clamping arithmetic);
 //  * lookup tables live in LDS at fixed addresses (table t at byte t*1024),
 //    built once per workgroup:
 //      4-bit: pair table, entry b = LUT[b & 15] | LUT[b >> 4] << 16, so one
@@ -32,7 +33,8 @@
 //    writes them to LDS; R*NB threads add the W wave totals and round once
 //    (RNE).
 // Only the last unit pass can be partial (U % T live threads); those lanes
-// skip it.  Requires K % 8 == 0 and 16-byte aligned x rows.
+// skip it.  Requires K % 8 == 0, 16-byte aligned x rows and an index block
+// (N * row bytes) below 2 GiB, so buffer offsets stay in 31 bits.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -75,6 +77,12 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
   return v;
 }
+
+// Buffer descriptor word 3 for gfx9-family (CDNA) raw buffers: 32-bit
+// data format, no swizzle; the range check is against num_records bytes.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer-load builtins: nontemporal.
+constexpr int kNontemporal = 2;
 
 // Minimum threads per workgroup by index width: the 8-bit LUT loads are
 // laid out for at least 256 threads (fewer still work, with more loads).
@@ -129,16 +137,22 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
     lreg[i] = lb[(size_t)rc * LUT_DW + dd % LUT_DW];
   }
 
-  // ---- x units
+  // ---- x units and the index units of the R rows, as buffer loads: one
+  // lane offset, the unit step as an immediate/scalar offset, and the
+  // descriptor's range check in place of address clamping (a unit past the
+  // end of x or of the index block reads as 0; lanes past the row's last
+  // unit never use theirs).  Index bytes are read once: nontemporal.
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
   uint32_t xr[NB][UPL][4];
 #pragma unroll
-  for (int t = 0; t < UPL; t++) {
-    const uint32_t u = (uint32_t)(tid + T * t);
-    const uint32_t cu = u < U ? u : U - 1;
+  for (int b = 0; b < NB; b++) {
+    const uint32_t bb = (uint32_t)b < a.nb ? (uint32_t)b : 0u;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (size_t)bb * K), (short)0, (int)(K * 2), kBufferWord3);
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-      const uint32_t bb = (uint32_t)b < a.nb ? (uint32_t)b : 0u;
-      const uint4 v = *reinterpret_cast<const uint4*>(a.x + (size_t)bb * K + (size_t)cu * 8);
+    for (int t = 0; t < UPL; t++) {
+      const u32x4v_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)tid * 16u, (uint32_t)(16 * T * t), 0);
       xr[b][t][0] = v.x;
       xr[b][t][1] = v.y;
       xr[b][t][2] = v.z;
@@ -146,24 +160,25 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
     }
   }
 
-  // ---- index units of the R rows, row by row (read once: nontemporal)
   uint32_t iv[R][NM][UPL][IW];
+  __amdgpu_buffer_rsrc_t ri[NM];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+    ri[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(m == 0 ? a.idx : a.idx2), (short)0, (int)(N * row_dw * 4u),
+                                              kBufferWord3);
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const uint32_t row = row0 + r;
     const uint32_t rc = row < N ? row : N - 1;
 #pragma unroll
     for (int m = 0; m < NM; m++) {
-      const uint32_t* base = reinterpret_cast<const uint32_t*>(m == 0 ? a.idx : a.idx2) + (size_t)rc * row_dw;
 #pragma unroll
       for (int t = 0; t < UPL; t++) {
-        const uint32_t u = (uint32_t)(tid + T * t);
-        const uint32_t cu = u < U ? u : U - 1;
+        const uint32_t so = rc * row_dw * 4u + (uint32_t)(4 * IW * T * t);
         if constexpr (IW == 1) {
-          iv[r][m][t][0] = __builtin_nontemporal_load(base + cu);
+          iv[r][m][t][0] = __builtin_amdgcn_raw_buffer_load_b32(ri[m], (uint32_t)tid * 4u, so, kNontemporal);
         } else {
-          typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-          const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(base) + cu);
+          const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(ri[m], (uint32_t)tid * 8u, so, kNontemporal);
           iv[r][m][t][0] = v.x;
           iv[r][m][t][1] = v.y;
         }

@@ -142,8 +142,10 @@ TilePlan tile_pick_upl(int upl, int threads) {
 
 // Rows per workgroup: 2 (4 tables for gate+up), 4 for 4+ batch vectors and
 // for 8-bit weights (whose LUT loads are spread over >= 256 threads).
-TilePlan plan_tile(uint32_t bits, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
+TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
   if (K % 8 != 0 || K == 0 || xaddr % 16 != 0) return TilePlan{};
+  // buffer descriptors address the index block and x with 32-bit ranges
+  if ((uint64_t)N * K * bits / 8 >= (1ull << 31) || (uint64_t)K * 2 >= (1ull << 31)) return TilePlan{};
   const uint32_t U = K / 8;
   const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
   if (dual && NB != 1) return TilePlan{};
@@ -194,7 +196,7 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
     a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
     a.nb = chunk;
-    const TilePlan p = plan_tile(bits, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
+    const TilePlan p = plan_tile(bits, N, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
     void* args[] = {&a};
     if (p.fn) {
       const uint32_t grid = (N + (uint32_t)p.R - 1) / (uint32_t)p.R;
