@@ -13,7 +13,10 @@ value = effective weight bytes (index + LUT bytes) x K / timed seconds.
 
 Other workloads (--workload): cfg1 (4-bit 4864x896), cfg2 (gate_up+SwiGLU
 2x18944x3584), cfg4 (8-bit 14336x4096, --batch B), cfg5 (prefill GEMM
-2048x4096x14336, TFLOP/s).
+2048x4096x14336, TFLOP/s), cfg3 (one decode step of a random-init
+Qwen2.5-0.5B-architecture model, 4-bit, KV length 512: tokens/s; a step is
+one token, KV rolled back to 512 after each so every step does the same
+work).
 """
 from __future__ import annotations
 
@@ -42,7 +45,9 @@ WORKLOADS = {
     "cfg2": ("gateup", 4, 18944, 3584, 1),
     "cfg4": ("gemv", 8, 14336, 4096, 1),
     "cfg5": ("gemm", 4, 14336, 4096, 2048),
+    "cfg3": ("decode", 4, 0, 0, 1),
 }
+DECODE_KV_LEN = 512
 
 
 def log(msg: str) -> None:
@@ -111,6 +116,110 @@ def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
             "cpu": cpu_model(), "host_cpus": os.cpu_count()}
 
 
+def run_decode(args, pe, seed) -> int:
+    """Config 3: the GPU-resident decode step (prism_hip_model_step_dev)."""
+    import torch
+    oracle = importlib.import_module("oracle")
+    cfg = pe.Qwen2Config()
+    L0 = DECODE_KV_LEN
+    log(f"[bench] workload=cfg3 decode step: Qwen2.5-0.5B architecture, 4-bit, KV {L0}, seed={seed}")
+    embed, layers = pe.synth_weights(cfg, seed)
+    emb_p, lay_p = pe.model.payloads(embed, layers)
+    kvs = pe.synth_kv(cfg, L0, seed)
+    ctx = pe.Context(0)
+    m = pe.Model.from_tensors(ctx, cfg, embed, layers, max_seq=L0 + 64)
+    for l, (k, v) in enumerate(kvs):
+        m.kv_append(l, k, v)
+    step_bytes = cfg.weight_bytes() + cfg.kv_bytes(L0)
+    log(f"[bench] {step_bytes / 1e6:.2f} MB read per token (weights {cfg.weight_bytes() / 1e6:.2f} MB + "
+        f"INT8 KV {cfg.kv_bytes(L0) / 1e6:.2f} MB)")
+
+    # parity guard: one step against the oracle (the tests hold the full bar)
+    kv = oracle.KVState(cfg.n_layers, cfg.kv_dim, L0 + 1)
+    for l, (k, v) in enumerate(kvs):
+        for t in range(L0):
+            kv.append(l, k[t], v[t])
+    got = m.step(42, L0)
+    want = oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv, 42, L0,
+                              threads=min(os.cpu_count() or 1, 16))
+    err = pe.rel_err(got, want)
+    log(f"[bench] parity check (logits) rel_err={err:.3e}")
+    if not err <= 1e-2:
+        log("[bench] PARITY FAILURE")
+        return 1
+    m.kv_truncate(L0)
+
+    stream = torch.cuda.Stream(device=torch.device("cuda", 0))
+
+    def step(i: int) -> None:
+        m.step_dev((i * 7919) % cfg.vocab, L0, stream)
+        m.kv_truncate(L0)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done")
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = e0.elapsed_time(e1)
+    ms_step = ms / args.steps
+    log(f"[bench] timed {args.steps} steps: {ms:.3f} ms on device events, {wall * 1e3:.3f} ms wall")
+    tps = 1e3 / ms_step
+    gbs = step_bytes / (ms_step * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline ...")
+        kv_c = oracle.KVState(cfg.n_layers, cfg.kv_dim, L0 + 1)
+        for l, (k, v) in enumerate(kvs):
+            for t in range(L0):
+                kv_c.append(l, k[t], v[t])
+        n, t0 = 0, time.perf_counter()
+        while n < 1 or time.perf_counter() - t0 < 8.0:
+            kv_c.len[:] = L0
+            oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv_c, 42 + n, L0, threads=1)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        cpu = {"value": round(1.0 / dt, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{n} decode steps at KV {L0} (oracle, 1 thread), {dt * 1e3:.0f} ms each",
+               "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+        log(f"[bench] cpu baseline {cpu['value']} tokens/s")
+
+    rec = {
+        "metric": "Qwen2.5-0.5B-architecture decode step tokens/s (4-bit palettized, batch 1, KV 512)",
+        "value": round(tps, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4-index/fp16-LUT, fp32 accumulate; INT8 KV",
+        "data": "synthetic (seeded PCG64: random-init weights, sorted N(0,0.02) fp16 LUTs, KV fp16 N(0,1))",
+        "config": {"workload": "cfg3", "kind": "decode", "layers": cfg.n_layers, "hidden": cfg.hidden,
+                   "heads": cfg.n_heads, "kv_heads": cfg.n_kv_heads, "intermediate": cfg.intermediate,
+                   "vocab": cfg.vocab, "kv_len": L0, "launch": "one HIP graph per token", "seed": seed},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode step (embed + 5 launches per layer + LM head, one graph)",
+                     "algorithmic_per_launch": step_bytes},
+        "cpu_baseline": cpu,
+        "parity_rel_err": err,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -136,6 +245,8 @@ def main() -> int:
     import torch
     pe = importlib.import_module("prism-engine_amd")
     kind, bits, N, K, batch = WORKLOADS[args.workload]
+    if kind == "decode":
+        return run_decode(args, pe, pe.SEEDS.get(args.workload, 1003))
     if args.batch is not None and kind == "gemv":
         batch = args.batch
     seed = pe.SEEDS.get(args.workload, 1000)
@@ -245,7 +356,8 @@ def main() -> int:
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None}
-    kernel_name = {"gemv": "k_gemv", "gateup": "k_gemv (DUAL gate_up)", "gemm": "k_gemm"}[kind]
+    kernel_name = {"gemv": "k_gemv_tile", "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
+                   "gemm": "k_gemm_w4" if bits == 4 else "k_gemm"}[kind]
     roof["kernel"] = kernel_name
     roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb
 

@@ -168,6 +168,70 @@ int prism_hip_backend_embed(prism_hip_backend* b, const char* key, uint32_t toke
 /* Number of registered tensors. */
 size_t prism_hip_backend_len(const prism_hip_backend* b);
 
+/* ---- GPU-resident decode step ----------------------------------------------
+ * Replaces PrismEngine::step (src/lut/engine_impl.rs:1076-1405) for the
+ * Qwen2 graph ModelGraph::build produces (src/lut/graph.rs:304-530), with
+ * the engine's INT8 KV cache (KVCache, engine_impl.rs:514-584) resident in
+ * HBM.  The engine's per-node CPU/GPU round trips (:160-188) become one HIP
+ * graph per token.  Semantics are the reference CPU path's: RMS norms
+ * without a norm weight (:1056-1065), RoPE on Q only with base 10000
+ * whatever rope_theta says (:1068-1075, :1211-1218), residual adds after
+ * o_proj and down_proj, silu(gate)*up, tied LM head = the embedding
+ * matrix (:1384-1403).  All projections are 4-bit split-block weights. */
+typedef struct prism_hip_model prism_hip_model;
+
+typedef struct prism_hip_model_config {
+  uint32_t n_layers;     /* num_hidden_layers                       */
+  uint32_t hidden;       /* hidden_size (multiple of 8)             */
+  uint32_t n_heads;      /* num_attention_heads                     */
+  uint32_t n_kv_heads;   /* num_key_value_heads (divides n_heads)   */
+  uint32_t head_dim;     /* 64                                      */
+  uint32_t intermediate; /* intermediate_size (multiple of 8)       */
+  uint32_t vocab;        /* vocab_size                              */
+  uint32_t max_seq;      /* KV capacity in tokens per layer         */
+  float rms_eps;         /* rms_norm_eps                            */
+  float rope_theta;      /* recorded; the CPU path rotates with 10000 */
+} prism_hip_model_config;
+
+/* Allocates the KV cache, activations and the RoPE table (generate()'s
+ * KVCache::new, engine_impl.rs:933-953).  NULL on error (context text). */
+prism_hip_model* prism_hip_model_create(prism_hip_ctx* ctx, const prism_hip_model_config* cfg);
+void prism_hip_model_free(prism_hip_model* m);
+
+/* Weights are copied into the model (QKV fused into one matrix), so the
+ * handles may be freed afterwards.  embed: [vocab x hidden] 4-bit, the
+ * TokenEmbedding tensor and the tied LM head (engine_impl.rs:1407-1446,
+ * :1384-1403).  Layer tensors in ModelGraph order (graph.rs:380-490). */
+int prism_hip_model_set_embedding(prism_hip_model* m, const prism_hip_weight* embed);
+int prism_hip_model_set_layer(prism_hip_model* m, uint32_t layer, const prism_hip_weight* q_proj,
+                              const prism_hip_weight* k_proj, const prism_hip_weight* v_proj,
+                              const prism_hip_weight* o_proj, const prism_hip_weight* gate_proj,
+                              const prism_hip_weight* up_proj, const prism_hip_weight* down_proj);
+
+/* KVCache::append(layer, k, v) for `ntokens` rows of kv_dim fp16 values
+ * each (host memory); every row becomes one INT8 block (engine_impl.rs:532-556). */
+int prism_hip_model_kv_append(prism_hip_model* m, uint32_t layer, const uint16_t* k, const uint16_t* v,
+                              uint32_t ntokens);
+/* Tokens cached in `layer` (KVCache::seq_len, engine_impl.rs:564-566). */
+int prism_hip_model_kv_len(const prism_hip_model* m, uint32_t layer, uint32_t* len);
+/* The layer's cache in the reference's byte format: len blocks of
+ * [scale f32 LE][kv_dim x i8] for K and for V (each len*(kv_dim+4) bytes). */
+int prism_hip_model_kv_read(prism_hip_model* m, uint32_t layer, uint8_t* k_blocks, uint8_t* v_blocks);
+int prism_hip_model_kv_reset(prism_hip_model* m);
+/* Forget every layer's tokens past `len` (a rollback; no device work).  The
+ * reference's KVCache only grows; this serves fixed-length benchmarks and
+ * callers that discard rejected tokens. */
+int prism_hip_model_kv_truncate(prism_hip_model* m, uint32_t len);
+
+/* One decode step: PrismEngine::step(token, pos) -> logits [vocab] fp16.
+ * Appends one KV token per layer.  pos < max_seq and every layer's KV
+ * length < max_seq.  _step copies the logits to host memory and waits;
+ * _step_dev only enqueues on `stream` (NULL: the context stream) and leaves
+ * the logits in the model's device buffer (prism_hip_model_logits_dev). */
+int prism_hip_model_step(prism_hip_model* m, uint32_t token, int64_t pos, uint16_t* logits);
+int prism_hip_model_step_dev(prism_hip_model* m, uint32_t token, int64_t pos, void* stream);
+const void* prism_hip_model_logits_dev(const prism_hip_model* m);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,24 @@ full list.  Parity status per function (what pins it):
 * ``silu``/``swiglu``: KAT evaluator.rs:286-298 and numpy float32 closed form.
 * ``lut_embed`` / ``decode_rows``: KAT evaluator.rs:267-284, nibble-order KAT
   palette.rs:410-425 and numpy unpack -- pinned.
+
+Decode step (``prism_cpuref_step.c``, the reference's PrismEngine::step for a
+Qwen2 graph):
+
+* ``rms_norm``: KAT evaluator.rs:249-257 (ones stay 1), constant-vector
+  closed form, numpy float64 bound, scale invariance -- pinned.
+* ``vec_add``: KAT evaluator.rs:258-265 and numpy float16 addition
+  (exhaustive over a grid) -- pinned.
+* ``rope``: pos 0 is the identity, pair j=0 rotates by exactly `pos`
+  radians (numpy float64 rotation), norm preservation, theta ignored --
+  pinned.
+* ``kv_quant`` / ``kv_dequant``: hand-computed blocks (round half away from
+  zero, clamp, zero-vector scale 1.0), round-trip bound max|x|/254 -- pinned.
+* ``attention``: one position returns v, equal keys return the mean of v,
+  numpy float64 softmax attention bound, GQA head mapping -- pinned.
+* ``decode_step``: recomposed in the tests from the pinned pieces above
+  following engine_impl.rs:1076-1405 (node order, Q-only RoPE, residual
+  placement, KV append) -- pinned by composition.
 """
 from __future__ import annotations
 
@@ -78,6 +96,26 @@ def lib():
         L.cpuref_decode_rows.argtypes = [_u8p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.c_uint32, ctypes.c_uint32, _u16p]
         L.cpuref_decode_rows.restype = ctypes.c_int
+        L.cpuref_rms_norm_inplace.argtypes = [_u16p, ctypes.c_size_t, ctypes.c_float]
+        L.cpuref_rms_norm_inplace.restype = None
+        L.cpuref_vec_add_inplace.argtypes = [_u16p, _u16p, ctypes.c_size_t]
+        L.cpuref_vec_add_inplace.restype = None
+        L.cpuref_rope_angle.argtypes = [ctypes.c_int64, ctypes.c_size_t, ctypes.c_size_t]
+        L.cpuref_rope_angle.restype = ctypes.c_float
+        L.cpuref_rope_inplace.argtypes = [_u16p, ctypes.c_size_t, ctypes.c_int64, ctypes.c_size_t]
+        L.cpuref_rope_inplace.restype = None
+        L.cpuref_kv_quant.argtypes = [_u16p, ctypes.c_size_t, _u8p]
+        L.cpuref_kv_quant.restype = ctypes.c_size_t
+        L.cpuref_kv_dequant.argtypes = [_u8p, ctypes.c_size_t, ctypes.c_size_t, _u16p]
+        L.cpuref_kv_dequant.restype = None
+        L.cpuref_attention.argtypes = [_u16p, _u16p, _u16p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                       ctypes.c_size_t, _u16p]
+        L.cpuref_attention.restype = None
+        L.cpuref_decode_step.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_float, _u8p,
+                                         ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p),
+                                         ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t),
+                                         ctypes.c_uint32, ctypes.c_int64, _u16p, ctypes.c_int]
+        L.cpuref_decode_step.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -193,3 +231,120 @@ def decode_rows(payload, dm, dn, bits, r0=0, nrows=None) -> np.ndarray:
     rc = lib().cpuref_decode_rows(_p8(payload), dm, dn, bits, r0, nrows, _p16(out))
     assert rc == 0
     return out
+
+
+# ---- decode step (prism_cpuref_step.c) -------------------------------------
+
+def rms_norm(x, eps: float) -> np.ndarray:
+    """rms_norm_inplace (evaluator.rs:49-64), on a copy."""
+    x = _bits16(x).copy()
+    lib().cpuref_rms_norm_inplace(_p16(x), x.size, ctypes.c_float(eps))
+    return x
+
+
+def vec_add(a, b) -> np.ndarray:
+    """vec_add_inplace (evaluator.rs:67-73), on a copy of a."""
+    a = _bits16(a).copy()
+    b = _bits16(b)
+    assert a.size == b.size
+    lib().cpuref_vec_add_inplace(_p16(a), _p16(b), a.size)
+    return a
+
+
+def rope_angle(pos: int, j: int, hd: int) -> float:
+    return float(lib().cpuref_rope_angle(pos, j, hd))
+
+
+def rope(x, pos: int, hd: int) -> np.ndarray:
+    """rope_inplace (evaluator.rs:154-166), on a copy; theta is not an
+    argument because the reference ignores it (base 10000)."""
+    x = _bits16(x).copy()
+    lib().cpuref_rope_inplace(_p16(x), x.size, pos, hd)
+    return x
+
+
+def kv_quant(data) -> np.ndarray:
+    """One INT8 KV token block [scale f32 LE][n x i8] (engine_impl.rs:532-556)."""
+    data = _bits16(data)
+    out = np.zeros(4 + data.size, dtype=np.uint8)
+    n = lib().cpuref_kv_quant(_p16(data), data.size, _p8(out))
+    return out[:n]
+
+
+def kv_dequant(blocks, ntok: int, kv_dim: int) -> np.ndarray:
+    """dequant_inline (engine_impl.rs:569-584) -> [ntok x kv_dim] fp16 bits."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    assert blocks.size >= ntok * (kv_dim + 4)
+    out = np.zeros((ntok, kv_dim), dtype=np.uint16)
+    lib().cpuref_kv_dequant(_p8(blocks), ntok, kv_dim, _p16(out))
+    return out
+
+
+def attention(q, kc, vc, nh: int, nkv: int, hd: int, sl: int) -> np.ndarray:
+    """attention_cpu (evaluator.rs:104-146); kc, vc [sl x nkv*hd] fp16 bits."""
+    q, kc, vc = _bits16(q), _bits16(kc), _bits16(vc)
+    out = np.zeros(nh * hd, dtype=np.uint16)
+    lib().cpuref_attention(_p16(q), _p16(kc), _p16(vc), nh, nkv, hd, sl, _p16(out))
+    return out
+
+
+class KVState:
+    """The reference's KVCache (engine_impl.rs:514-584): per layer, INT8
+    token blocks of (4 + kv_dim) bytes for K and for V."""
+
+    def __init__(self, n_layers: int, kv_dim: int, capacity: int):
+        self.kv_dim = kv_dim
+        self.capacity = capacity
+        ts = kv_dim + 4
+        self.k = [np.zeros(capacity * ts, dtype=np.uint8) for _ in range(n_layers)]
+        self.v = [np.zeros(capacity * ts, dtype=np.uint8) for _ in range(n_layers)]
+        self.len = np.zeros(n_layers, dtype=np.uintp)
+
+    def append(self, layer: int, k, v) -> None:
+        """KVCache::append(l, k, v) with both slices given: one block each."""
+        ts = self.kv_dim + 4
+        n = int(self.len[layer])
+        assert n < self.capacity
+        self.k[layer][n * ts:(n + 1) * ts] = kv_quant(k)
+        self.v[layer][n * ts:(n + 1) * ts] = kv_quant(v)
+        self.len[layer] = n + 1
+
+    def dequant(self, layer: int):
+        n = int(self.len[layer])
+        return (kv_dequant(self.k[layer], n, self.kv_dim), kv_dequant(self.v[layer], n, self.kv_dim))
+
+    def copy(self) -> "KVState":
+        c = KVState.__new__(KVState)
+        c.kv_dim, c.capacity = self.kv_dim, self.capacity
+        c.k = [a.copy() for a in self.k]
+        c.v = [a.copy() for a in self.v]
+        c.len = self.len.copy()
+        return c
+
+
+def decode_step(dims, eps: float, embed, layers, kv: KVState, token: int, pos: int,
+                threads: int = 1) -> np.ndarray:
+    """PrismEngine::step (engine_impl.rs:1076-1405) for a Qwen2 graph.
+
+    dims = (n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate,
+    vocab, bits); `layers` is a list of 7-payload tuples (q, k, v, o, gate,
+    up, down); `embed` the [vocab x hidden] 4-bit embedding (tied LM head).
+    Advances `kv` by one token per layer and returns the fp16 logits."""
+    L = int(dims[0])
+    assert len(layers) == L and len(kv.k) == L
+    d = (ctypes.c_uint32 * 8)(*[int(v) for v in dims])
+    ws = [np.ascontiguousarray(w, dtype=np.uint8) for lw in layers for w in lw]
+    wp = (ctypes.c_void_p * max(1, len(ws)))(*[w.ctypes.data for w in ws])
+    kp = (ctypes.c_void_p * max(1, L))(*[a.ctypes.data for a in kv.k])
+    vp = (ctypes.c_void_p * max(1, L))(*[a.ctypes.data for a in kv.v])
+    for l in range(L):
+        assert int(kv.len[l]) < kv.capacity
+    lens = (ctypes.c_size_t * max(1, L))(*[int(v) for v in kv.len])
+    embed = np.ascontiguousarray(embed, dtype=np.uint8)
+    logits = np.zeros(int(dims[6]), dtype=np.uint16)
+    rc = lib().cpuref_decode_step(d, ctypes.c_float(eps), _p8(embed), wp, kp, vp, lens, token, pos,
+                                  _p16(logits), threads)
+    assert rc == 0, rc
+    for l in range(L):
+        kv.len[l] = lens[l]
+    return logits

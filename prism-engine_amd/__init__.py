@@ -10,7 +10,8 @@ The directory name is not a Python identifier; import it with
 ``importlib.import_module("prism-engine_amd")``.
 """
 from ._native import PrismHipError, header_functions, load as load_library  # noqa: F401
-from .backend import Context, HipBackend, Weight, load_cimage  # noqa: F401
+from .backend import Context, HipBackend, Model, Weight, load_cimage  # noqa: F401
+from .model import Qwen2Config, synth_kv, synth_weights, tensor_names  # noqa: F401
 from .cimage import CImageReader, CImageWriter  # noqa: F401
 from .palette import (  # noqa: F401
     SEEDS,

@@ -34,6 +34,18 @@ _u16p = _c.POINTER(_c.c_uint16)
 _u32p = _c.POINTER(_c.c_uint32)
 _szp = _c.POINTER(_c.c_size_t)
 
+
+
+class ModelConfig(ctypes.Structure):
+    """prism_hip_model_config (include/prism_hip.h)."""
+    _fields_ = [("n_layers", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("n_heads", ctypes.c_uint32),
+                ("n_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32), ("intermediate", ctypes.c_uint32),
+                ("vocab", ctypes.c_uint32), ("max_seq", ctypes.c_uint32), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float)]
+
+
+_cfgp = ctypes.POINTER(ModelConfig)
+
 # name -> (restype, argtypes); must cover every function in prism_hip.h
 SIGNATURES = {
     "prism_hip_ctx_create": (_vp, [_c.c_int]),
@@ -64,6 +76,18 @@ SIGNATURES = {
     "prism_hip_backend_gemm": (_c.c_int, [_vp, _c.c_char_p, _vp, _c.c_uint32, _vp]),
     "prism_hip_backend_embed": (_c.c_int, [_vp, _c.c_char_p, _c.c_uint32, _vp, _c.c_size_t]),
     "prism_hip_backend_len": (_c.c_size_t, [_vp]),
+    "prism_hip_model_create": (_vp, [_vp, _cfgp]),
+    "prism_hip_model_free": (None, [_vp]),
+    "prism_hip_model_set_embedding": (_c.c_int, [_vp, _vp]),
+    "prism_hip_model_set_layer": (_c.c_int, [_vp, _c.c_uint32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "prism_hip_model_kv_append": (_c.c_int, [_vp, _c.c_uint32, _vp, _vp, _c.c_uint32]),
+    "prism_hip_model_kv_len": (_c.c_int, [_vp, _c.c_uint32, _u32p]),
+    "prism_hip_model_kv_read": (_c.c_int, [_vp, _c.c_uint32, _vp, _vp]),
+    "prism_hip_model_kv_reset": (_c.c_int, [_vp]),
+    "prism_hip_model_kv_truncate": (_c.c_int, [_vp, _c.c_uint32]),
+    "prism_hip_model_step": (_c.c_int, [_vp, _c.c_uint32, _c.c_int64, _vp]),
+    "prism_hip_model_step_dev": (_c.c_int, [_vp, _c.c_uint32, _c.c_int64, _vp]),
+    "prism_hip_model_logits_dev": (_vp, [_vp]),
 }
 
 _lib = None

@@ -7,6 +7,8 @@
   ``fused_gate_up(gate_key, up_key, input, output)``, plus ``gemm`` and
   ``embed``.  Where the reference returns ``Err(String)`` this raises
   :class:`PrismHipError` with the same text ("miss <key>", ...).
+* :class:`Model` wraps ``prism_hip_model``: the GPU-resident decode step
+  (PrismEngine::step, engine_impl.rs:1076-1405) with its INT8 KV cache.
 * :func:`load_cimage` uploads every palettized tensor of a `.cimage` file
   (the weight half of ``PrismEngine::load`` + ``MetalBackend::new``,
   engine_impl.rs:597-636,124-133).
@@ -16,6 +18,7 @@ raises; there is no fallback path.
 """
 from __future__ import annotations
 
+import ctypes
 import sys
 
 import numpy as np
@@ -145,6 +148,93 @@ class Weight:
             return
         try:
             self.free()
+        except Exception:
+            pass
+
+
+class Model:
+    """prism_hip_model: one decode step per call, KV cache in HBM."""
+
+    def __init__(self, ctx: Context, cfg, max_seq: int = 4096):
+        self.ctx, self.cfg, self.max_seq = ctx, cfg, max_seq
+        c = _native.ModelConfig(cfg.n_layers, cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                cfg.intermediate, cfg.vocab, max_seq, cfg.rms_eps, cfg.rope_theta)
+        self.h = ctx.lib.prism_hip_model_create(ctx.h, ctypes.byref(c))
+        if not self.h:
+            raise PrismHipError(_native.ERR_SHAPE, ctx.error())
+
+    @classmethod
+    def from_tensors(cls, ctx: Context, cfg, embed: PalettizedTensor, layers, max_seq: int = 4096) -> "Model":
+        """Upload `embed` and the per-layer tensors (7 per layer, q k v o gate
+        up down); the model keeps its own copies."""
+        m = cls(ctx, cfg, max_seq)
+        w = ctx.upload_tensor(embed)
+        m.set_embedding(w)
+        w.free()
+        for l, lw in enumerate(layers):
+            ws = [ctx.upload_tensor(t) for t in lw]
+            m.set_layer(l, ws)
+            for x in ws:
+                x.free()
+        return m
+
+    def set_embedding(self, w: "Weight") -> None:
+        self.ctx.check(self.ctx.lib.prism_hip_model_set_embedding(self.h, w.h))
+
+    def set_layer(self, layer: int, ws) -> None:
+        assert len(ws) == 7
+        self.ctx.check(self.ctx.lib.prism_hip_model_set_layer(self.h, layer, *[w.h for w in ws]))
+
+    def kv_append(self, layer: int, k, v) -> None:
+        """KVCache::append for rows of kv_dim fp16 values (k, v: [n, kv_dim])."""
+        k, v = _u16(k), _u16(v)
+        n = k.size // self.cfg.kv_dim
+        assert k.size == v.size == n * self.cfg.kv_dim
+        self.ctx.check(self.ctx.lib.prism_hip_model_kv_append(self.h, layer, k.ctypes.data, v.ctypes.data, n))
+
+    def kv_len(self, layer: int) -> int:
+        n = ctypes.c_uint32(0)
+        self.ctx.check(self.ctx.lib.prism_hip_model_kv_len(self.h, layer, ctypes.byref(n)))
+        return int(n.value)
+
+    def kv_read(self, layer: int):
+        """(K blocks, V blocks) in the reference's byte format."""
+        n = self.kv_len(layer)
+        kb = np.zeros(n * (self.cfg.kv_dim + 4), dtype=np.uint8)
+        vb = np.zeros_like(kb)
+        self.ctx.check(self.ctx.lib.prism_hip_model_kv_read(self.h, layer, kb.ctypes.data, vb.ctypes.data))
+        return kb, vb
+
+    def kv_reset(self) -> None:
+        self.ctx.check(self.ctx.lib.prism_hip_model_kv_reset(self.h))
+
+    def kv_truncate(self, n: int) -> None:
+        """Drop every layer's tokens past n (host bookkeeping only)."""
+        self.ctx.check(self.ctx.lib.prism_hip_model_kv_truncate(self.h, n))
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        """PrismEngine::step(token, pos): fp16 logits [vocab] (host)."""
+        out = np.empty(self.cfg.vocab, dtype=np.uint16)
+        self.ctx.check(self.ctx.lib.prism_hip_model_step(self.h, token, pos, out.ctypes.data))
+        return out
+
+    def step_dev(self, token: int, pos: int, stream=None) -> None:
+        """Enqueue one step on `stream`; logits stay in logits_dev()."""
+        self.ctx.check(self.ctx.lib.prism_hip_model_step_dev(self.h, token, pos, _stream_handle(stream)))
+
+    def logits_dev(self) -> int:
+        return int(self.ctx.lib.prism_hip_model_logits_dev(self.h) or 0)
+
+    def close(self) -> None:
+        if self.h:
+            self.ctx.lib.prism_hip_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.close()
         except Exception:
             pass
 

@@ -55,6 +55,7 @@ struct GemvArgs {
   uint32_t N;
   uint32_t K;
   uint32_t nb;          // live batch rows (<= NB)
+  float eps;            // RMS-norm epsilon (k_gemv_tile with kEpiNorm)
 };
 
 // Generic kernel for shapes the tiled kernel does not take (K % 8 != 0,

@@ -78,6 +78,18 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   return v;
 }
 
+// Prologue / epilogue options of k_gemv_tile (bit flags; NB must be 1):
+//  kEpiNorm  x is RMS-normalised first, rms_norm_inplace
+//            (compute-core/src/lut/evaluator.rs:49-64) without a norm
+//            weight: inv = 1 / sqrt(sum(x^2) / K + eps), x <- f16(x * inv).
+//            Every workgroup holds all of x across its lanes, so it sums the
+//            squares of its own units and reduces across its waves.
+//  kEpiResid y is the residual stream, updated in place:
+//            y[row] <- f16(f16(acc) + y[row]) (vec_add_inplace after the
+//            projection, src/lut/engine_impl.rs:1158-1162,1208-1213).
+constexpr int kEpiNorm = 1;
+constexpr int kEpiResid = 2;
+
 // Buffer descriptor word 3 for gfx9-family (CDNA) raw buffers: 32-bit
 // data format, no swizzle; the range check is against num_records bytes.
 constexpr int kBufferWord3 = 0x00020000;
@@ -98,11 +110,13 @@ constexpr size_t gemv_tile_lds_bytes(int threads) {
   const size_t tables = (size_t)NT * 256;
   const size_t stage = (BITS == 4) ? (size_t)NT * 8 + threads : (size_t)2 * threads;
   const size_t parts = (size_t)(threads / 64) * NT * NB;
-  return 4 * (tables + stage + parts);
+  const size_t norm = (size_t)(threads / 64);
+  return 4 * (tables + stage + parts + norm);
 }
 
-template <int BITS, int UPL, int R, bool DUAL, int NB>
+template <int BITS, int UPL, int R, bool DUAL, int NB, int EPI = 0>
 __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
+  static_assert(EPI == 0 || NB == 1, "norm / residual options are single-vector");
   constexpr int NM = DUAL ? 2 : 1;
   constexpr int NT = NM * R;                 // lookup tables (matrix-major)
   constexpr int IW = (BITS == 4) ? 1 : 2;    // index dwords per unit
@@ -110,7 +124,7 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   static_assert(NT <= 16, "table offsets must stay within 16 KB");
   extern __shared__ uint32_t lds[];          // dynamic LDS only: starts at address 0
   // LDS: [NT tables x 256 dwords][4-bit: NT*8 staged LUT dwords + T scratch |
-  //       8-bit: 2T scratch][W * NT * NB partial sums]
+  //       8-bit: 2T scratch][W * NT * NB partial sums][W norm partials]
 
   const int T = blockDim.x;
   const int W = T >> 6;
@@ -121,6 +135,7 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   const uint32_t row0 = blockIdx.x * R;
   uint32_t* stage = lds + NT * 256;
   float* part = reinterpret_cast<float*>(stage + ((BITS == 4) ? NT * 8 + T : 2 * T));
+  float* nsum = part + W * NT * NB;
 
   // ---- LUT dwords of the NT rows (matrix-major, contiguous per matrix)
   constexpr int LUT_TOTAL = NT * LUT_DW;
@@ -218,6 +233,33 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   }
   __syncthreads();
 
+  if constexpr ((EPI & kEpiNorm) != 0) {
+    // sum of squares of this thread's units (units past K read as 0)
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < UPL; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float lo = h2f((uint16_t)(xr[0][t][e] & 0xFFFFu)), hi = h2f((uint16_t)(xr[0][t][e] >> 16));
+        ss += lo * lo;
+        ss += hi * hi;
+      }
+    ss = wave_sum_to_lane63(ss);
+    if (lane == 63) nsum[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int w = 0; w < W; w++) tot += nsum[w];
+    const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
+#pragma unroll
+    for (int t = 0; t < UPL; t++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t lo = f2h(h2f((uint16_t)(xr[0][t][e] & 0xFFFFu)) * inv);
+        const uint32_t hi = f2h(h2f((uint16_t)(xr[0][t][e] >> 16)) * inv);
+        xr[0][t][e] = lo | (hi << 16);
+      }
+  }
+
   const bool last_live = (uint32_t)(tid + T * (UPL - 1)) < U;
   float acc[R][NM][NB];
 #pragma unroll
@@ -273,6 +315,8 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
     if (row < N && (uint32_t)b < a.nb) {
       if constexpr (DUAL)
         a.y[row] = swiglu_h(s[0], s[NM - 1]);
+      else if constexpr ((EPI & kEpiResid) != 0)
+        a.y[row] = f2h(h2f(f2h(s[0])) + h2f(a.y[row]));
       else
         a.y[(size_t)b * N + row] = f2h(s[0]);
     }

@@ -19,6 +19,7 @@
 #include "gemm_kernels.hpp"
 #include "gemv_kernels.hpp"
 #include "gemv_tile.hpp"
+#include "step_kernels.hpp"
 
 #define PRISM_HIP_VERSION "prism_hip 0.1 gfx950"
 
@@ -32,7 +33,12 @@ struct prism_hip_ctx {
   // Weights uploaded through this context; destroying the context orphans
   // them (w->ctx = nullptr) so a later prism_hip_weight_free stays valid.
   std::unordered_set<prism_hip_weight*> weights;
+  // Decode-step models created on this context, orphaned the same way.
+  std::unordered_set<prism_hip_model*> models;
 };
+
+// Defined with prism_hip_model (model_step.hpp): forget the context.
+static void model_detach(prism_hip_model* m);
 
 struct prism_hip_weight {
   prism_hip_ctx* ctx = nullptr;
@@ -117,10 +123,10 @@ struct TilePlan {
   size_t lds = 0;
 };
 
-template <int BITS, int UPL, int R, bool DUAL, int NB>
+template <int BITS, int UPL, int R, bool DUAL, int NB, int EPI>
 TilePlan tile_entry(int threads) {
   TilePlan p;
-  p.fn = reinterpret_cast<const void*>(&prism::k_gemv_tile<BITS, UPL, R, DUAL, NB>);
+  p.fn = reinterpret_cast<const void*>(&prism::k_gemv_tile<BITS, UPL, R, DUAL, NB, EPI>);
   p.threads = threads;
   p.R = R;
   p.lds = prism::gemv_tile_lds_bytes<BITS, R, DUAL, NB>(threads);
@@ -128,12 +134,12 @@ TilePlan tile_entry(int threads) {
 }
 
 // x units held in VGPRs: NB * UPL * 4 registers, at most 64.
-template <int BITS, int R, bool DUAL, int NB>
+template <int BITS, int R, bool DUAL, int NB, int EPI = 0>
 TilePlan tile_pick_upl(int upl, int threads) {
   switch (upl) {
 #define PRISM_TU(u) \
   case u:           \
-    if constexpr (NB * (u) <= 16) return tile_entry<BITS, u, R, DUAL, NB>(threads); else return TilePlan{};
+    if constexpr (NB * (u) <= 16) return tile_entry<BITS, u, R, DUAL, NB, EPI>(threads); else return TilePlan{};
     PRISM_TU(1) PRISM_TU(2) PRISM_TU(3) PRISM_TU(4) PRISM_TU(5) PRISM_TU(6) PRISM_TU(7) PRISM_TU(8)
 #undef PRISM_TU
   }
@@ -142,18 +148,24 @@ TilePlan tile_pick_upl(int upl, int threads) {
 
 // Rows per workgroup: 2 (4 tables for gate+up), 4 for 4+ batch vectors and
 // for 8-bit weights (whose LUT loads are spread over >= 256 threads).
-TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr) {
+// `epi` (prism::kEpiNorm / kEpiResid, decode step only) is 4-bit, batch 1.
+TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr, int epi = 0) {
   if (K % 8 != 0 || K == 0 || xaddr % 16 != 0) return TilePlan{};
   // buffer descriptors address the index block and x with 32-bit ranges
   if ((uint64_t)N * K * bits / 8 >= (1ull << 31) || (uint64_t)K * 2 >= (1ull << 31)) return TilePlan{};
   const uint32_t U = K / 8;
   const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
   if (dual && NB != 1) return TilePlan{};
+  if (epi && (NB != 1 || bits != 4)) return TilePlan{};
   const uint32_t uplmax = (uint32_t)(16 / NB < 8 ? 16 / NB : 8);
+  // Very tall single-vector 4-bit matrices (an LM head: N >= 32768) take 4
+  // rows per workgroup: at 2 rows, dispatching N/2 workgroups costs more
+  // than their bytes (measured on 151936 x 896: 47 us at R=2, 26 us at R=4).
+  const bool tall = bits == 4 && NB == 1 && !dual && N >= 32768;
   // waves per workgroup: the fewest that keep UPL <= uplmax; 4-bit rows of
-  // 65..128 units (K <= 1024) use 2 waves, 8-bit ones at least 4
+  // 65..128 units (K <= 1024) use 2 waves unless tall, 8-bit ones at least 4
   uint32_t W = 0;
-  const uint32_t wmin = bits == 8 ? 4u : (U > 64 && U <= 128 && NB == 1) ? 2u : 1u;
+  const uint32_t wmin = bits == 8 ? 4u : (U > 64 && U <= 128 && NB == 1 && !tall) ? 2u : 1u;
   for (uint32_t w = wmin; w <= 8; w *= 2)
     if ((U + 64 * w - 1) / (64 * w) <= uplmax) {
       W = w;
@@ -163,7 +175,20 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
   const int upl = (int)((U + 64 * W - 1) / (64 * W));
   const int threads = (int)(64 * W);
   if (bits == 4) {
-    if (dual) return tile_pick_upl<4, 2, true, 1>(upl, threads);
+    if (dual) {
+      if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, true, 1, prism::kEpiNorm>(upl, threads);
+      if (epi) return TilePlan{};
+      return tile_pick_upl<4, 2, true, 1>(upl, threads);
+    }
+    if (tall) {
+      if (epi == prism::kEpiNorm) return tile_pick_upl<4, 4, false, 1, prism::kEpiNorm>(upl, threads);
+      if (epi == prism::kEpiResid) return tile_pick_upl<4, 4, false, 1, prism::kEpiResid>(upl, threads);
+      if (epi) return TilePlan{};
+      return tile_pick_upl<4, 4, false, 1>(upl, threads);
+    }
+    if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, false, 1, prism::kEpiNorm>(upl, threads);
+    if (epi == prism::kEpiResid) return tile_pick_upl<4, 2, false, 1, prism::kEpiResid>(upl, threads);
+    if (epi) return TilePlan{};
     switch (NB) {
       case 1: return tile_pick_upl<4, 2, false, 1>(upl, threads);
       case 2: return tile_pick_upl<4, 2, false, 2>(upl, threads);
@@ -180,28 +205,33 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
   }
 }
 
-int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
-                uint32_t nb, void* d_y, hipStream_t st) {
-  const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
-  const bool dual = (w2 != nullptr);
+// GEMV over raw split-block device pointers (lut2/idx2 non-null: gate+up
+// with the SwiGLU epilogue).  `epi` selects the decode step's fused norm /
+// residual forms, which have no generic fallback.
+int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, const uint8_t* lut,
+                    const uint8_t* idx, const uint8_t* lut2, const uint8_t* idx2, const void* d_x, uint32_t nb,
+                    void* d_y, hipStream_t st, int epi = 0, float eps = 0.0f) {
+  const bool dual = (lut2 != nullptr);
   prism::GemvArgs a;
-  a.lut = w->lut();
-  a.idx = w->idx();
-  a.lut2 = dual ? w2->lut() : nullptr;
-  a.idx2 = dual ? w2->idx() : nullptr;
+  a.lut = lut;
+  a.idx = idx;
+  a.lut2 = lut2;
+  a.idx2 = idx2;
   a.N = N;
   a.K = K;
+  a.eps = eps;
   for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
     const uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
     a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
     a.nb = chunk;
-    const TilePlan p = plan_tile(bits, N, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x));
+    const TilePlan p = plan_tile(bits, N, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x), epi);
     void* args[] = {&a};
     if (p.fn) {
       const uint32_t grid = (N + (uint32_t)p.R - 1) / (uint32_t)p.R;
       HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(p.threads), args, p.lds, st));
     } else {
+      if (epi) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no fused kernel for %u-bit %ux%u", bits, N, K);
       const void* fn;
       if (dual)
         fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, true>)
@@ -213,6 +243,12 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
     }
   }
   return PRISM_HIP_OK;
+}
+
+int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
+                uint32_t nb, void* d_y, hipStream_t st) {
+  return launch_gemv_raw(ctx, w->bits, w->dim_m, w->dim_n, w->lut(), w->idx(), w2 ? w2->lut() : nullptr,
+                         w2 ? w2->idx() : nullptr, d_x, nb, d_y, st);
 }
 
 int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
@@ -319,6 +355,8 @@ void prism_hip_ctx_destroy(prism_hip_ctx* ctx) {
   DeviceGuard g(ctx->device);
   for (prism_hip_weight* w : ctx->weights) w->ctx = nullptr;
   ctx->weights.clear();
+  for (prism_hip_model* m : ctx->models) model_detach(m);
+  ctx->models.clear();
   if (ctx->stream) {
     (void)hipStreamSynchronize(ctx->stream);
     (void)hipStreamDestroy(ctx->stream);
@@ -534,3 +572,6 @@ int prism_hip_lut_embed(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t 
 }
 
 }  // extern "C"
+
+// GPU-resident decode step (prism_hip_model_*).
+#include "model_step.hpp"

@@ -1,0 +1,290 @@
+// step_kernels.hpp -- the non-GEMV kernels of the GPU-resident decode step
+// (PrismEngine::step, src/lut/engine_impl.rs:1076-1405, for a Qwen2 graph).
+//
+// Per token the step runs: k_step_embed; per layer the QKV GEMV (RMS norm
+// in its prologue), k_step_attention, the O GEMV (+ residual), the gate/up
+// SwiGLU GEMV (RMS norm in its prologue), the down GEMV (+ residual); the
+// LM-head GEMV (RMS norm in its prologue).  Everything that changes from
+// token to token (token id, position, KV lengths) is read from a StepParams
+// block in device memory, so the launch sequence is fixed and replays as
+// one HIP graph.
+//
+// KV cache: the reference's INT8 cache (KVCache, engine_impl.rs:514-584),
+// kept in HBM as two planes per layer and matrix: int8 values
+// [max_seq][kv_dim] and one fp32 scale per token; a block of the
+// reference's byte format is (scale, values).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemv_kernels.hpp"
+
+namespace prism {
+
+constexpr int kMaxLayers = 128;
+
+struct StepParams {
+  uint32_t token;
+  uint32_t pos;
+  uint32_t kv_len[kMaxLayers];  // tokens cached per layer before this step
+};
+
+__global__ void k_step_set_params(StepParams v, StepParams* dst) {
+  if (threadIdx.x == 0) *dst = v;
+}
+
+// Embedding row of the step's token: lut_embed (compute-core/src/lut/
+// evaluator.rs:176-197; engine_impl.rs:1407-1446): LUT[token][nibble] for
+// the first (D/8)*8 elements, zeros past them and for tokens >= vocab.
+__global__ __launch_bounds__(256) void k_step_embed(const uint8_t* __restrict__ emb, uint32_t vocab, uint32_t D,
+                                                    const StepParams* __restrict__ sp, uint16_t* __restrict__ h) {
+  const uint32_t tok = sp->token;
+  const uint32_t keff = (D / 8) * 8;
+  for (uint32_t k = threadIdx.x; k < D; k += blockDim.x) {
+    uint16_t v = 0;
+    if (tok < vocab && k < keff) {
+      const uint8_t b = emb[(size_t)vocab * 32 + (size_t)tok * (D / 2) + k / 2];
+      const uint32_t nib = (k & 1) ? (b >> 4) : (b & 15u);
+      const uint8_t* l = emb + (size_t)tok * 32 + 2 * nib;
+      v = (uint16_t)(l[0] | (l[1] << 8));
+    }
+    h[k] = v;
+  }
+}
+
+// ---- INT8 KV quantization (KVCache::append's q(), engine_impl.rs:532-556)
+
+// Block-wide max of |x| over n fp16 values held one per thread (threads past
+// n pass 0).  `red` holds one float per wave.
+__device__ __forceinline__ float block_max(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float m = red[0];
+  for (int w = 1; w < nw; w++) m = fmaxf(m, red[w]);
+  return m;
+}
+
+// scale = 127 / max|x| (1.0 when max|x| <= 1e-10); q = clamp(round(x * scale)),
+// round half away from zero like f32::round.
+__device__ __forceinline__ float kv_scale(float max_abs) { return max_abs > 1e-10f ? 127.0f / max_abs : 1.0f; }
+__device__ __forceinline__ int8_t kv_q(float x, float scale) {
+  float q = roundf(x * scale);
+  q = fminf(fmaxf(q, -128.0f), 127.0f);
+  return (int8_t)q;
+}
+// dequant_inline (engine_impl.rs:569-584): f16(q * (1 / s)).
+__device__ __forceinline__ float kv_dq(int8_t q, float rs) { return h2f(f2h((float)q * rs)); }
+
+// Quantize `ntok` fp16 rows of kv_dim values into cache slots first, first+1,
+// ...: one workgroup per row, kv_dim <= blockDim.x.
+__global__ __launch_bounds__(256) void k_kv_quant_rows(const uint16_t* __restrict__ src, uint32_t ntok,
+                                                       uint32_t kv_dim, int8_t* __restrict__ q,
+                                                       float* __restrict__ scale, uint32_t first) {
+  __shared__ float red[4];
+  const uint32_t t = blockIdx.x;
+  if (t >= ntok) return;
+  const uint32_t i = threadIdx.x;
+  const float x = i < kv_dim ? h2f(src[(size_t)t * kv_dim + i]) : 0.0f;
+  const float s = kv_scale(block_max(fabsf(x), red));
+  if (i < kv_dim) q[(size_t)(first + t) * kv_dim + i] = kv_q(x, s);
+  if (i == 0) scale[first + t] = s;
+}
+
+// ---- attention step
+
+struct AttnArgs {
+  const uint16_t* qkv;     // [nh*hd q | kv_dim k | kv_dim v] fp16, this token
+  int8_t* kq;              // this layer's K values [max_seq][kv_dim]
+  float* ks;               // K scales [max_seq]
+  int8_t* vq;
+  float* vs;
+  const float2* rope;      // (cos, sin) [max_seq][hd/2]
+  const StepParams* sp;
+  uint16_t* out;           // [nh*hd] fp16
+  uint32_t layer;
+  uint32_t nh, nkv;
+};
+
+// One workgroup per query head, kAttnThreads threads, HD = 64.  Follows
+// the engine's step for one layer from the K/V projections to the
+// attention output:
+//  * the new token's K and V (whole kv_dim vectors, one scale each) are
+//    quantized like KVCache::append; workgroup 0 writes them to slot
+//    kv_len; every workgroup uses its own dequantized copy for that slot,
+//    so no workgroup waits for another;
+//  * RoPE on the head's q only (the engine never rotates K,
+//    engine_impl.rs:1211-1218), pair (j, j+32) by the host-built
+//    (cos, sin) of pos * 10000^(-2j/64) (evaluator.rs:154-166);
+//  * attention_cpu (evaluator.rs:104-146) over sl = kv_len + 1 positions,
+//    in passes of kAttnThreads positions:
+//      scores: thread t takes position base + t; its K row (64 bytes of
+//        this head) is a sequential fp32 dot of fp16 q and dequantized fp16
+//        k in the reference's order, divided by sqrt(64);
+//      values: lane l of wave w takes dims 4*(l%16)..+3 of positions
+//        base + 4w + l/16 + 64j, so every V load is a contiguous 256-byte
+//        wave access; 4 lanes per dim group are summed with two shuffles
+//        and the waves through LDS;
+//    the first pass's K rows, V words and scales are loaded before the
+//    quantization and RoPE, so their latency overlaps that work.  The
+//    softmax keeps a running max and sum across passes; the output is
+//    scaled once by 1 / (sum + 1e-10).  Max is exact; the exp, the sums and
+//    the output are fp32 in another order than the reference's folds.
+constexpr int kAttnMaxSeq = 8192;
+constexpr int kAttnThreads = 1024;
+__global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
+#pragma clang fp contract(off)
+  constexpr int HD = 64;
+  constexpr int T = kAttnThreads;
+  constexpr int NW = T / 64;
+  constexpr int VJ = T / 64;  // V words per lane per pass (4 positions x 16 dim groups per wave)
+  __shared__ float s_q[HD];
+  __shared__ float s_knew[HD], s_vnew[HD];
+  __shared__ float s_red[2 * NW];
+  __shared__ float s_e[T];
+  __shared__ float s_out[NW][HD];
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t h = blockIdx.x;
+  const uint32_t kvd = a.nkv * HD;
+  const uint32_t kvh = h / (a.nh / a.nkv);
+  const uint32_t len0 = a.sp->kv_len[a.layer];
+  const uint32_t pos = a.sp->pos;
+  const uint32_t sl = len0 + 1;
+  const uint32_t last = len0 ? len0 - 1 : 0;  // clamp target for unused loads
+  const uint16_t* qh = a.qkv + (size_t)h * HD;
+  const uint16_t* knew = a.qkv + (size_t)a.nh * HD;
+  const uint16_t* vnew = knew + kvd;
+  const uint32_t dg = lane & 15, psub = lane >> 4;  // V: dim group, position in the wave's 4
+
+  uint4 kr[HD / 16];
+  float krs;
+  uint32_t vw[VJ];
+  float vrs[VJ];
+  auto load_pass = [&](uint32_t base) {
+    const uint32_t p = base + tid;
+    const uint32_t pc = p < len0 ? p : last;
+    const uint4* kp = reinterpret_cast<const uint4*>(a.kq + (size_t)pc * kvd + kvh * HD);
+#pragma unroll
+    for (int i = 0; i < HD / 16; i++) kr[i] = kp[i];
+    krs = a.ks[pc];
+#pragma unroll
+    for (int j = 0; j < VJ; j++) {
+      const uint32_t pv = base + 4 * wave + psub + 64 * j;
+      const uint32_t pvc = pv < len0 ? pv : last;
+      vw[j] = *reinterpret_cast<const uint32_t*>(a.vq + (size_t)pvc * kvd + kvh * HD + 4 * dg);
+      vrs[j] = a.vs[pvc];
+    }
+  };
+  load_pass(0);
+
+  // ---- new token's K and V: scale over all kv_dim values (kvd <= 256)
+  const float kx = tid < kvd ? h2f(knew[tid]) : 0.0f;
+  const float vx = tid < kvd ? h2f(vnew[tid]) : 0.0f;
+  const float ksc = kv_scale(block_max(fabsf(kx), s_red));
+  const float vsc = kv_scale(block_max(fabsf(vx), s_red + NW));
+  const int8_t kq8 = kv_q(kx, ksc), vq8 = kv_q(vx, vsc);
+  if (tid < kvd) {
+    if (h == 0) {
+      a.kq[(size_t)len0 * kvd + tid] = kq8;
+      a.vq[(size_t)len0 * kvd + tid] = vq8;
+    }
+    if (tid >= kvh * HD && tid < (kvh + 1) * HD) {
+      s_knew[tid - kvh * HD] = kv_dq(kq8, 1.0f / ksc);
+      s_vnew[tid - kvh * HD] = kv_dq(vq8, 1.0f / vsc);
+    }
+  }
+  if (h == 0 && tid == 0) {
+    a.ks[len0] = ksc;
+    a.vs[len0] = vsc;
+  }
+
+  // ---- RoPE on q (pairs j, j + 32)
+  if (tid < HD / 2) {
+    const float2 cs = a.rope[(size_t)pos * (HD / 2) + tid];
+    const float x0 = h2f(qh[tid]), x1 = h2f(qh[tid + HD / 2]);
+    s_q[tid] = h2f(f2h(x0 * cs.x - x1 * cs.y));
+    s_q[tid + HD / 2] = h2f(f2h(x0 * cs.y + x1 * cs.x));
+  }
+  __syncthreads();
+
+  const float den = sqrtf((float)HD);
+  float m_run = -INFINITY, s_run = 0.0f;
+  float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t base = 0; base < sl; base += T) {
+    if (base) {
+      __syncthreads();  // s_e of the previous pass is consumed
+      load_pass(base);
+    }
+    // ---- score of position base + tid
+    const uint32_t p = base + tid;
+    float sc = -INFINITY;
+    if (p < len0) {
+      const float rs = 1.0f / krs;
+      const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kr[0]);
+      float s = 0.0f;
+#pragma unroll
+      for (int d = 0; d < HD; d++) s += s_q[d] * kv_dq((int8_t)(kw[d / 4] >> (8 * (d % 4))), rs);
+      sc = s / den;
+    } else if (p == len0) {
+      float s = 0.0f;
+#pragma unroll
+      for (int d = 0; d < HD; d++) s += s_q[d] * s_knew[d];
+      sc = s / den;
+    }
+    const float m_new = fmaxf(m_run, block_max(sc, s_red));
+    const float corr = expf(m_run - m_new);  // 0 on the first pass
+    const float e = (p < sl) ? expf(sc - m_new) : 0.0f;
+    s_e[tid] = e;
+    float esum = e;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) esum += __shfl_xor(esum, off, 64);
+    __syncthreads();  // s_e complete; s_red free
+    if (lane == 0) s_red[NW + wave] = esum;
+    __syncthreads();
+    float bsum = 0.0f;
+    for (int w = 0; w < NW; w++) bsum += s_red[NW + w];
+    s_run = s_run * corr + bsum;
+    m_run = m_new;
+    // ---- values
+#pragma unroll
+    for (int c = 0; c < 4; c++) o4[c] *= corr;
+#pragma unroll
+    for (int j = 0; j < VJ; j++) {
+      const uint32_t pv = base + 4 * wave + psub + 64 * j;
+      if (pv >= sl) continue;
+      const float ev = s_e[pv - base];
+      if (pv < len0) {
+        const float rs = 1.0f / vrs[j];
+#pragma unroll
+        for (int c = 0; c < 4; c++) o4[c] += ev * kv_dq((int8_t)(vw[j] >> (8 * c)), rs);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; c++) o4[c] += ev * s_vnew[4 * dg + c];
+      }
+    }
+  }
+  const float inv = 1.0f / (s_run + 1e-10f);
+
+  // ---- sum over the 4 position lanes of each dim group, then over waves
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    o4[c] += __shfl_xor(o4[c], 16, 64);
+    o4[c] += __shfl_xor(o4[c], 32, 64);
+  }
+  if (psub == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) s_out[wave][4 * dg + c] = o4[c];
+  }
+  __syncthreads();
+  if (tid < HD) {
+    float v = 0.0f;
+    for (int w = 0; w < NW; w++) v += s_out[w][tid];
+    a.out[(size_t)h * HD + tid] = f2h(v * inv);
+  }
+}
+
+}  // namespace prism
