@@ -56,6 +56,7 @@ struct GemvArgs {
   uint32_t K;
   uint32_t nb;          // live batch rows (<= NB)
   float eps;            // RMS-norm epsilon (k_gemv_tile with kEpiNorm)
+  const float* xpart;   // attention split partials (k_gemv_tile with kEpiAttnIn)
 };
 
 // Generic kernel for shapes the tiled kernel does not take (K % 8 != 0,

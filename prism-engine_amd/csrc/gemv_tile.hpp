@@ -40,6 +40,7 @@
 #include <stdint.h>
 
 #include "gemv_kernels.hpp"
+#include "step_kernels.hpp"
 
 namespace prism {
 
@@ -87,8 +88,14 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
 //  kEpiResid y is the residual stream, updated in place:
 //            y[row] <- f16(f16(acc) + y[row]) (vec_add_inplace after the
 //            projection, src/lut/engine_impl.rs:1158-1162,1208-1213).
+//  kEpiAttnIn x is the attention output of the decode step, given as the
+//            split partials of k_step_attention (a.xpart, [K/64 heads]
+//            [kAttnSplits][2 + 64] fp32): each thread combines its own units
+//            (head u/8, dims 8*(u%8)..+7) and rounds them to fp16, the value
+//            k_step_attn_combine would store.
 constexpr int kEpiNorm = 1;
 constexpr int kEpiResid = 2;
+constexpr int kEpiAttnIn = 4;
 
 // Buffer descriptor word 3 for gfx9-family (CDNA) raw buffers: 32-bit
 // data format, no swizzle; the range check is against num_records bytes.
@@ -160,6 +167,20 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
   typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
   uint32_t xr[NB][UPL][4];
+  if constexpr ((EPI & kEpiAttnIn) != 0) {
+#pragma unroll
+    for (int t = 0; t < UPL; t++) {
+      const uint32_t u = (uint32_t)(tid + T * t);
+      const uint32_t cu = u < U ? u : U - 1;
+      const float* hp = a.xpart + (size_t)(cu / 8) * kAttnSplits * 66;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t lo = f2h(attn_combine(hp, 8 * (cu % 8) + 2 * e));
+        const uint32_t hi = f2h(attn_combine(hp, 8 * (cu % 8) + 2 * e + 1));
+        xr[0][t][e] = lo | (hi << 16);
+      }
+    }
+  } else
 #pragma unroll
   for (int b = 0; b < NB; b++) {
     const uint32_t bb = (uint32_t)b < a.nb ? (uint32_t)b : 0u;

@@ -15,8 +15,8 @@
 //                    reference's rope_inplace calls -- so the device
 //                    rotation uses the reference's angles bit for bit
 //   activations      residual stream h [hidden], q|k|v [nqkv], attention
-//                    output [nh*64], SwiGLU output [intermediate], logits
-//                    [vocab] fp16; StepParams
+//                    split partials [nh][kAttnSplits][66] fp32, SwiGLU output
+//                    [intermediate], logits [vocab] fp16; StepParams
 // One step = k_step_set_params (token, pos, KV lengths) + one graph replay
 // of the fixed launch sequence (captured once per weight set).
 #pragma once
@@ -39,10 +39,10 @@ struct prism_hip_model {
   float2* rope = nullptr;
   uint16_t* hres = nullptr;
   uint16_t* qkv_out = nullptr;
-  uint16_t* attn = nullptr;
   uint16_t* act = nullptr;
   uint16_t* logits = nullptr;
   prism::StepParams* d_params = nullptr;
+  float* attn_part = nullptr;     // k_step_attention split partials
   std::vector<uint32_t> kv_len;
   hipStream_t cap_stream = nullptr;
   hipGraph_t graph = nullptr;
@@ -121,15 +121,18 @@ int model_enqueue(prism_hip_model* m, hipStream_t st) {
     aa.vs = m->vs + (size_t)l * c.max_seq;
     aa.rope = m->rope;
     aa.sp = m->d_params;
-    aa.out = m->attn;
+    aa.part = m->attn_part;
     aa.layer = l;
     aa.nh = c.n_heads;
     aa.nkv = c.n_kv_heads;
-    hipLaunchKernelGGL(prism::k_step_attention, dim3(c.n_heads), dim3(prism::kAttnThreads), 0, st, aa);
+    hipLaunchKernelGGL(prism::k_step_attention, dim3(c.n_heads * prism::kAttnSplits), dim3(prism::kAttnThreads), 0,
+                       st, aa);
     HIP_TRY(ctx, hipGetLastError());
+    // O projection: x = the attention output, combined from the split
+    // partials in the GEMV's prologue; residual add in its epilogue
     const uint8_t* wo = m->o[l];
-    if ((rc = launch_gemv_raw(ctx, 4, D, m->qd, wo, wo + (size_t)D * 32, nullptr, nullptr, m->attn, 1, m->hres, st,
-                              prism::kEpiResid)))
+    if ((rc = launch_gemv_raw(ctx, 4, D, m->qd, wo, wo + (size_t)D * 32, nullptr, nullptr, nullptr, 1, m->hres, st,
+                              prism::kEpiAttnIn | prism::kEpiResid, 0.0f, m->attn_part)))
       return rc;
     const uint8_t* wg = m->gate[l];
     const uint8_t* wu = m->up[l];
@@ -207,10 +210,11 @@ prism_hip_model* prism_hip_model_create(prism_hip_ctx* ctx, const prism_hip_mode
   if (!rc) rc = model_alloc(m, &m->rope, (size_t)c.max_seq * 32 * sizeof(float2));
   if (!rc) rc = model_alloc(m, &m->hres, (size_t)D * 2);
   if (!rc) rc = model_alloc(m, &m->qkv_out, (size_t)m->nqkv * 2);
-  if (!rc) rc = model_alloc(m, &m->attn, (size_t)m->qd * 2);
   if (!rc) rc = model_alloc(m, &m->act, (size_t)I * 2);
   if (!rc) rc = model_alloc(m, &m->logits, (size_t)c.vocab * 2);
   if (!rc) rc = model_alloc(m, &m->d_params, sizeof(prism::StepParams));
+  if (!rc) rc = model_alloc(m, &m->attn_part, (size_t)c.n_heads * prism::kAttnSplits * (2 + 64) * 4);
+
   if (!rc) {
     // RoPE angles pos * 10000^(-2j/64) with the C library's powf/sinf/cosf,
     // exactly as rope_inplace computes them (evaluator.rs:154-166).

@@ -148,7 +148,8 @@ TilePlan tile_pick_upl(int upl, int threads) {
 
 // Rows per workgroup: 2 (4 tables for gate+up), 4 for 4+ batch vectors and
 // for 8-bit weights (whose LUT loads are spread over >= 256 threads).
-// `epi` (prism::kEpiNorm / kEpiResid, decode step only) is 4-bit, batch 1.
+// `epi` (prism::kEpiNorm, kEpiResid, kEpiAttnIn | kEpiResid; decode step
+// only) is 4-bit, batch 1.
 TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual, uintptr_t xaddr, int epi = 0) {
   if (K % 8 != 0 || K == 0 || xaddr % 16 != 0) return TilePlan{};
   // buffer descriptors address the index block and x with 32-bit ranges
@@ -188,6 +189,8 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
     }
     if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, false, 1, prism::kEpiNorm>(upl, threads);
     if (epi == prism::kEpiResid) return tile_pick_upl<4, 2, false, 1, prism::kEpiResid>(upl, threads);
+    if (epi == (prism::kEpiAttnIn | prism::kEpiResid))
+      return tile_pick_upl<4, 2, false, 1, prism::kEpiAttnIn | prism::kEpiResid>(upl, threads);
     if (epi) return TilePlan{};
     switch (NB) {
       case 1: return tile_pick_upl<4, 2, false, 1>(upl, threads);
@@ -210,7 +213,7 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
 // residual forms, which have no generic fallback.
 int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, const uint8_t* lut,
                     const uint8_t* idx, const uint8_t* lut2, const uint8_t* idx2, const void* d_x, uint32_t nb,
-                    void* d_y, hipStream_t st, int epi = 0, float eps = 0.0f) {
+                    void* d_y, hipStream_t st, int epi = 0, float eps = 0.0f, const float* xpart = nullptr) {
   const bool dual = (lut2 != nullptr);
   prism::GemvArgs a;
   a.lut = lut;
@@ -220,6 +223,7 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
   a.N = N;
   a.K = K;
   a.eps = eps;
+  a.xpart = xpart;
   for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
     const uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;

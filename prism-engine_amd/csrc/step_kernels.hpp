@@ -104,43 +104,48 @@ struct AttnArgs {
   float* vs;
   const float2* rope;      // (cos, sin) [max_seq][hd/2]
   const StepParams* sp;
-  uint16_t* out;           // [nh*hd] fp16
+  float* part;             // split partials [nh][kAttnSplits][2 + hd] (max, sum, unnormalised out)
   uint32_t layer;
   uint32_t nh, nkv;
 };
 
-// One workgroup per query head, kAttnThreads threads, HD = 64.  Follows
-// the engine's step for one layer from the K/V projections to the
-// attention output:
-//  * the new token's K and V (whole kv_dim vectors, one scale each) are
-//    quantized like KVCache::append; workgroup 0 writes them to slot
-//    kv_len; every workgroup uses its own dequantized copy for that slot,
-//    so no workgroup waits for another;
+// kAttnSplits workgroups per query head (flash decoding), kAttnThreads
+// threads each, HD = 64.  Follows the engine's step for one layer from the K/V projections
+// to the attention output:
 //  * RoPE on the head's q only (the engine never rotates K,
 //    engine_impl.rs:1211-1218), pair (j, j+32) by the host-built
 //    (cos, sin) of pos * 10000^(-2j/64) (evaluator.rs:154-166);
-//  * attention_cpu (evaluator.rs:104-146) over sl = kv_len + 1 positions,
-//    in passes of kAttnThreads positions:
-//      scores: thread t takes position base + t; its K row (64 bytes of
-//        this head) is a sequential fp32 dot of fp16 q and dequantized fp16
-//        k in the reference's order, divided by sqrt(64);
-//      values: lane l of wave w takes dims 4*(l%16)..+3 of positions
-//        base + 4w + l/16 + 64j, so every V load is a contiguous 256-byte
-//        wave access; 4 lanes per dim group are summed with two shuffles
-//        and the waves through LDS;
-//    the first pass's K rows, V words and scales are loaded before the
-//    quantization and RoPE, so their latency overlaps that work.  The
-//    softmax keeps a running max and sum across passes; the output is
-//    scaled once by 1 / (sum + 1e-10).  Max is exact; the exp, the sums and
-//    the output are fp32 in another order than the reference's folds.
-constexpr int kAttnMaxSeq = 8192;
-constexpr int kAttnThreads = 1024;
+//  * the new token's K and V (whole kv_dim vectors, one scale each) are
+//    quantized like KVCache::append by the workgroups whose range holds
+//    position kv_len; the one of head 0 writes them to slot kv_len, and each
+//    uses its own dequantized copy, so no workgroup waits for another;
+//  * attention_cpu (evaluator.rs:104-146) over sl = kv_len + 1 positions:
+//    split s of a head takes positions [s*C, (s+1)*C), C = ceil(sl / S).
+//    Scores: one position per thread, a sequential fp32 dot of fp16 q and
+//    dequantized fp16 k in the reference's order, divided by sqrt(64).
+//    Values: lane l owns dims 4*(l%16)..+3 of positions l/16 + 4j (4w +
+//    l/16 + 4*W*j for W waves), so every V load is a contiguous 256-byte
+//    wave access.
+//    A split writes (m, sum_p e^(s_p - m), sum_p e^(s_p - m) v_p) to `part`;
+//    the O-projection GEMV's prologue (kEpiAttnIn, attn_combine) rescales
+//    the S partials to the head's max, adds them and scales once by
+//    1 / (sum + 1e-10); the kernel boundary makes every split's partial
+//    visible (device-scope fences inside this kernel would write back and
+//    invalidate each XCD's whole L2).  Max is exact; the exp, the
+//    sums and the output are fp32 in another order than the reference's folds.
+// Every global K/V load of a split is issued before the new token's
+// quantization and RoPE.  sl <= kAttnSplits * kAttnThreads * kAttnPasses.
+constexpr int kAttnSplits = 4;
+constexpr int kAttnThreads = 256;
+constexpr int kAttnPasses = 8;
+constexpr int kAttnMaxSeq = kAttnSplits * kAttnThreads * kAttnPasses;
 __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
 #pragma clang fp contract(off)
   constexpr int HD = 64;
   constexpr int T = kAttnThreads;
   constexpr int NW = T / 64;
-  constexpr int VJ = T / 64;  // V words per lane per pass (4 positions x 16 dim groups per wave)
+  constexpr int S = kAttnSplits;
+  constexpr int VJ = T / (4 * NW);  // V words per lane per pass: positions 4w + l/16 + 4*NW*j
   __shared__ float s_q[HD];
   __shared__ float s_knew[HD], s_vnew[HD];
   __shared__ float s_red[2 * NW];
@@ -148,17 +153,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
   __shared__ float s_out[NW][HD];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t h = blockIdx.x;
+  const uint32_t h = blockIdx.x / S, sp = blockIdx.x % S;
   const uint32_t kvd = a.nkv * HD;
   const uint32_t kvh = h / (a.nh / a.nkv);
   const uint32_t len0 = a.sp->kv_len[a.layer];
   const uint32_t pos = a.sp->pos;
   const uint32_t sl = len0 + 1;
-  const uint32_t last = len0 ? len0 - 1 : 0;  // clamp target for unused loads
+  const uint32_t C = (sl + S - 1) / S;
+  const uint32_t p0 = sp * C;
+  const uint32_t p1 = p0 + C < sl ? p0 + C : sl;
+  const bool has_new = p0 <= len0 && len0 < p1;  // uniform per workgroup
+  const uint32_t last = len0 ? len0 - 1 : 0;    // clamp target for unused loads
   const uint16_t* qh = a.qkv + (size_t)h * HD;
   const uint16_t* knew = a.qkv + (size_t)a.nh * HD;
   const uint16_t* vnew = knew + kvd;
-  const uint32_t dg = lane & 15, psub = lane >> 4;  // V: dim group, position in the wave's 4
+  const uint32_t dg = lane & 15, psub = lane >> 4;
 
   uint4 kr[HD / 16];
   float krs;
@@ -173,33 +182,38 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
     krs = a.ks[pc];
 #pragma unroll
     for (int j = 0; j < VJ; j++) {
-      const uint32_t pv = base + 4 * wave + psub + 64 * j;
+      const uint32_t pv = base + 4 * wave + psub + 4 * NW * j;
       const uint32_t pvc = pv < len0 ? pv : last;
       vw[j] = *reinterpret_cast<const uint32_t*>(a.vq + (size_t)pvc * kvd + kvh * HD + 4 * dg);
       vrs[j] = a.vs[pvc];
     }
   };
-  load_pass(0);
+  if (p0 < p1) load_pass(p0);
 
-  // ---- new token's K and V: scale over all kv_dim values (kvd <= 256)
-  const float kx = tid < kvd ? h2f(knew[tid]) : 0.0f;
-  const float vx = tid < kvd ? h2f(vnew[tid]) : 0.0f;
-  const float ksc = kv_scale(block_max(fabsf(kx), s_red));
-  const float vsc = kv_scale(block_max(fabsf(vx), s_red + NW));
-  const int8_t kq8 = kv_q(kx, ksc), vq8 = kv_q(vx, vsc);
-  if (tid < kvd) {
+  // ---- new token's K and V (only the splits holding position kv_len):
+  // kv_dim values per matrix, strided over the workgroup's threads
+  if (has_new) {
+    float kmax = 0.0f, vmax = 0.0f;
+    for (uint32_t i = tid; i < kvd; i += T) {
+      kmax = fmaxf(kmax, fabsf(h2f(knew[i])));
+      vmax = fmaxf(vmax, fabsf(h2f(vnew[i])));
+    }
+    const float ksc = kv_scale(block_max(kmax, s_red));
+    const float vsc = kv_scale(block_max(vmax, s_red + NW));
     if (h == 0) {
-      a.kq[(size_t)len0 * kvd + tid] = kq8;
-      a.vq[(size_t)len0 * kvd + tid] = vq8;
+      for (uint32_t i = tid; i < kvd; i += T) {
+        a.kq[(size_t)len0 * kvd + i] = kv_q(h2f(knew[i]), ksc);
+        a.vq[(size_t)len0 * kvd + i] = kv_q(h2f(vnew[i]), vsc);
+      }
+      if (tid == 0) {
+        a.ks[len0] = ksc;
+        a.vs[len0] = vsc;
+      }
     }
-    if (tid >= kvh * HD && tid < (kvh + 1) * HD) {
-      s_knew[tid - kvh * HD] = kv_dq(kq8, 1.0f / ksc);
-      s_vnew[tid - kvh * HD] = kv_dq(vq8, 1.0f / vsc);
+    for (uint32_t i = tid; i < (uint32_t)HD; i += T) {
+      s_knew[i] = kv_dq(kv_q(h2f(knew[kvh * HD + i]), ksc), 1.0f / ksc);
+      s_vnew[i] = kv_dq(kv_q(h2f(vnew[kvh * HD + i]), vsc), 1.0f / vsc);
     }
-  }
-  if (h == 0 && tid == 0) {
-    a.ks[len0] = ksc;
-    a.vs[len0] = vsc;
   }
 
   // ---- RoPE on q (pairs j, j + 32)
@@ -214,48 +228,46 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
   const float den = sqrtf((float)HD);
   float m_run = -INFINITY, s_run = 0.0f;
   float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (uint32_t base = 0; base < sl; base += T) {
-    if (base) {
+  for (uint32_t base = p0; base < p1; base += T) {
+    if (base != p0) {
       __syncthreads();  // s_e of the previous pass is consumed
       load_pass(base);
     }
-    // ---- score of position base + tid
     const uint32_t p = base + tid;
     float sc = -INFINITY;
-    if (p < len0) {
-      const float rs = 1.0f / krs;
-      const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kr[0]);
-      float s = 0.0f;
+    if (p < p1) {
+      float sdot = 0.0f;
+      if (p < len0) {
+        const float rs = 1.0f / krs;
+        const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kr[0]);
 #pragma unroll
-      for (int d = 0; d < HD; d++) s += s_q[d] * kv_dq((int8_t)(kw[d / 4] >> (8 * (d % 4))), rs);
-      sc = s / den;
-    } else if (p == len0) {
-      float s = 0.0f;
+        for (int d = 0; d < HD; d++) sdot += s_q[d] * kv_dq((int8_t)(kw[d / 4] >> (8 * (d % 4))), rs);
+      } else {
 #pragma unroll
-      for (int d = 0; d < HD; d++) s += s_q[d] * s_knew[d];
-      sc = s / den;
+        for (int d = 0; d < HD; d++) sdot += s_q[d] * s_knew[d];
+      }
+      sc = sdot / den;
     }
     const float m_new = fmaxf(m_run, block_max(sc, s_red));
     const float corr = expf(m_run - m_new);  // 0 on the first pass
-    const float e = (p < sl) ? expf(sc - m_new) : 0.0f;
+    const float e = (p < p1) ? expf(sc - m_new) : 0.0f;
     s_e[tid] = e;
     float esum = e;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) esum += __shfl_xor(esum, off, 64);
-    __syncthreads();  // s_e complete; s_red free
+    __syncthreads();
     if (lane == 0) s_red[NW + wave] = esum;
     __syncthreads();
     float bsum = 0.0f;
     for (int w = 0; w < NW; w++) bsum += s_red[NW + w];
     s_run = s_run * corr + bsum;
     m_run = m_new;
-    // ---- values
 #pragma unroll
     for (int c = 0; c < 4; c++) o4[c] *= corr;
 #pragma unroll
     for (int j = 0; j < VJ; j++) {
-      const uint32_t pv = base + 4 * wave + psub + 64 * j;
-      if (pv >= sl) continue;
+      const uint32_t pv = base + 4 * wave + psub + 4 * NW * j;
+      if (pv >= p1) continue;
       const float ev = s_e[pv - base];
       if (pv < len0) {
         const float rs = 1.0f / vrs[j];
@@ -267,9 +279,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
       }
     }
   }
-  const float inv = 1.0f / (s_run + 1e-10f);
 
-  // ---- sum over the 4 position lanes of each dim group, then over waves
+  // ---- this split's partial: (m, sum, unnormalised output)
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     o4[c] += __shfl_xor(o4[c], 16, 64);
@@ -280,11 +291,37 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
     for (int c = 0; c < 4; c++) s_out[wave][4 * dg + c] = o4[c];
   }
   __syncthreads();
+  float* mypart = a.part + ((size_t)h * S + sp) * (2 + HD);
   if (tid < HD) {
     float v = 0.0f;
     for (int w = 0; w < NW; w++) v += s_out[w][tid];
-    a.out[(size_t)h * HD + tid] = f2h(v * inv);
+    mypart[2 + tid] = v;
   }
+  if (tid == 0) {
+    mypart[0] = m_run;
+    mypart[1] = s_run;
+  }
+}
+
+// Attention output element (head h, dim d) from the head's S split partials
+// [S][2 + 64]: rescale to the head's max, add, scale once by 1/(sum + 1e-10).
+__device__ __forceinline__ float attn_combine(const float* hp, uint32_t d) {
+#pragma clang fp contract(off)
+  constexpr int S = kAttnSplits;
+  float mi[S];
+#pragma unroll
+  for (int i = 0; i < S; i++) mi[i] = hp[i * 66];
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < S; i++) M = fmaxf(M, mi[i]);
+  float tot = 0.0f, o = 0.0f;
+#pragma unroll
+  for (int i = 0; i < S; i++) {
+    const float f = (mi[i] == -INFINITY) ? 0.0f : expf(mi[i] - M);
+    tot += hp[i * 66 + 1] * f;
+    o += hp[i * 66 + 2 + d] * f;
+  }
+  return o * (1.0f / (tot + 1e-10f));
 }
 
 }  // namespace prism

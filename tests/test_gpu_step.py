@@ -82,6 +82,26 @@ def test_step_tiny_matches_oracle(gpu_ctx, token, pos, n_cached):
         assert np.max(np.abs(new_g - new_o)) <= 2
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(4, 2), (4, 4), (6, 2)])
+def test_step_kv_widths_match_oracle(gpu_ctx, heads, kv_heads):
+    """kv_dim 128 and 256 (up to the 256 limit) and grouped heads 3:1."""
+    cfg = pe.Qwen2Config(**{**TINY, "n_heads": heads, "n_kv_heads": kv_heads, "hidden": 64 * heads})
+    m, emb_p, lay_p, kv = build(gpu_ctx, cfg, 33, 20)
+    print(f"heads {heads}/{kv_heads}", flush=True)
+    got = m.step(7, 20)
+    want = oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv, 7, 20, threads=4)
+    err = pe.rel_err(got, want)
+    print(f"  logits rel err {err:.3e}", flush=True)
+    assert err <= STEP_TOL
+    for l in range(cfg.n_layers):
+        kb, vb = m.kv_read(l)
+        ts = cfg.kv_dim + 4
+        assert np.array_equal(kb[:20 * ts], kv.k[l][:20 * ts])
+        new_g = kb[20 * ts + 4:21 * ts].view(np.int8).astype(int)
+        new_o = kv.k[l][20 * ts + 4:21 * ts].view(np.int8).astype(int)
+        assert np.max(np.abs(new_g - new_o)) <= 2
+
+
 def test_step_sequence_matches_oracle(gpu_ctx):
     cfg = pe.Qwen2Config(**TINY)
     m, emb_p, lay_p, kv = build(gpu_ctx, cfg, 41, 3)
