@@ -136,6 +136,23 @@ int prism_hip_lut_embed(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t 
 int prism_hip_decode_rows_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, uint32_t nrows,
                               void* d_out, void* stream);
 
+/* ---- palette compiler ---------------------------------------------------- */
+
+/* k-means palettization of an fp32 [out_dim x in_dim] row-major matrix into
+ * the split-block payload: out_dim x 16 fp16 LUT entries (zero past k),
+ * then every row's packed 4-bit indices, (in_dim+1)/2 bytes per row
+ * (prism_hip_palettize_bytes in all).  Replaces palettize_matrix
+ * (src/quantization/palette.rs:230-272: fit_palette :75-183 with the
+ * threshold of :186-191, encode_channel :198-228) plus compile_to_cimage's
+ * payload assembly (src/lut/compiler.rs:47-60, called with k=16,
+ * max_iter=50); the payload is byte-identical to the reference's.
+ * k must be 1..16 (PRISM_HIP_ERR_SHAPE otherwise). */
+size_t prism_hip_palettize_bytes(uint32_t out_dim, uint32_t in_dim);
+int prism_hip_palettize(prism_hip_ctx* ctx, const float* w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
+                        uint32_t max_iter, uint8_t* payload);
+int prism_hip_palettize_dev(prism_hip_ctx* ctx, const void* d_w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
+                            uint32_t max_iter, void* d_payload, void* stream);
+
 /* ---- keyed backend (MetalBackend's surface) ------------------------------ */
 
 /* A name -> weight map over one context, mirroring MetalBackend

@@ -36,6 +36,18 @@ Qwen2 graph):
 * ``decode_step``: recomposed in the tests from the pinned pieces above
   following engine_impl.rs:1076-1405 (node order, Q-only RoPE, residual
   placement, KV append) -- pinned by composition.
+
+Palette compiler (``prism_cpuref_palette.c``, fit_palette / encode_channel /
+palettize_matrix and compile_to_cimage's payload):
+
+* ``encode_channel``: KAT palette.rs:410-425 (0x10, 0x32, MSE 0), brute-force
+  argmin over the codebook on random data -- pinned.
+* ``fit_palette``: KATs palette.rs:373-408 (three clusters), :495-523 (empty,
+  constant channel); invariants (sorted by magnitude, fixed point of one Lloyd
+  step when converged, k = min(k, n)); a numpy restatement of the k-means++
+  pick on small inputs -- pinned.
+* ``palettize_payload``: KATs palette.rs:427-492 (3x4 round trip, 64x128 MSE
+  bound), layout of compiler.rs:47-60 -- pinned.
 """
 from __future__ import annotations
 
@@ -116,6 +128,14 @@ def lib():
                                          ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t),
                                          ctypes.c_uint32, ctypes.c_int64, _u16p, ctypes.c_int]
         L.cpuref_decode_step.restype = ctypes.c_int
+        _f32p = ctypes.POINTER(ctypes.c_float)
+        L.cpuref_fit_palette.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _f32p]
+        L.cpuref_fit_palette.restype = ctypes.c_size_t
+        L.cpuref_encode_channel.argtypes = [_f32p, ctypes.c_size_t, _f32p, ctypes.c_size_t, _u8p]
+        L.cpuref_encode_channel.restype = ctypes.c_float
+        L.cpuref_palettize_payload.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                               ctypes.c_size_t, _u8p, _f32p]
+        L.cpuref_palettize_payload.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -348,3 +368,61 @@ def decode_step(dims, eps: float, embed, layers, kv: KVState, token: int, pos: i
     for l in range(L):
         kv.len[l] = lens[l]
     return logits
+
+
+# ---- palette compiler (prism_cpuref_palette.c) -----------------------------
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def fit_palette(channel, k: int = 16, max_iter: int = 50) -> np.ndarray:
+    """fit_palette (palette.rs:75-183): min(k, n) centroids, |c| descending."""
+    ch = _f32(channel)
+    out = np.zeros(max(k, 1), dtype=np.float32)
+    kc = lib().cpuref_fit_palette(ch.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), ch.size, k, max_iter,
+                                  out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return out[:kc].copy()
+
+
+def encode_channel(channel, codebook):
+    """encode_channel (palette.rs:198-228): (packed indices, MSE)."""
+    ch = _f32(channel)
+    cb = _f32(codebook)
+    packed = np.zeros((ch.size + 1) // 2, dtype=np.uint8)
+    mse = lib().cpuref_encode_channel(ch.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), ch.size,
+                                      cb.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), cb.size, _p8(packed))
+    return packed, float(mse)
+
+
+def palettize_payload(weights, k: int = 16, max_iter: int = 50, threads: int = 1):
+    """palettize_matrix + compile_to_cimage's payload (compiler.rs:47-60) for a
+    [out_dim, in_dim] f32 matrix: (payload bytes, per-row MSE)."""
+    w = _f32(weights)
+    assert w.ndim == 2
+    out_dim, in_dim = w.shape
+    payload = np.zeros(out_dim * 32 + out_dim * ((in_dim + 1) // 2), dtype=np.uint8)
+    mse = np.zeros(out_dim, dtype=np.float32)
+    fp = ctypes.POINTER(ctypes.c_float)
+    if threads <= 1 or out_dim < 2 * threads:
+        rc = lib().cpuref_palettize_payload(w.ctypes.data_as(fp), out_dim, in_dim, k, max_iter, _p8(payload),
+                                            mse.ctypes.data_as(fp))
+        assert rc == 0
+        return payload, mse
+    # rows are independent: split them over host threads (identical bytes)
+    from concurrent.futures import ThreadPoolExecutor
+    bounds = np.linspace(0, out_dim, threads + 1).astype(int)
+    parts = []
+
+    def run(a, b):
+        p, e = palettize_payload(w[a:b], k, max_iter, 1)
+        return a, b, p, e
+
+    with ThreadPoolExecutor(threads) as ex:
+        parts = list(ex.map(lambda ab: run(*ab), zip(bounds[:-1], bounds[1:])))
+    rb = (in_dim + 1) // 2
+    for a, b, p, e in parts:
+        payload[a * 32:b * 32] = p[:(b - a) * 32]
+        payload[out_dim * 32 + a * rb:out_dim * 32 + b * rb] = p[(b - a) * 32:]
+        mse[a:b] = e
+    return payload, mse

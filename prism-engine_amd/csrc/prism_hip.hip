@@ -9,6 +9,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -19,6 +20,7 @@
 #include "gemm_kernels.hpp"
 #include "gemv_kernels.hpp"
 #include "gemv_tile.hpp"
+#include "palette_kernels.hpp"
 #include "step_kernels.hpp"
 
 #define PRISM_HIP_VERSION "prism_hip 0.1 gfx950"
@@ -27,6 +29,7 @@ struct prism_hip_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   int num_cu = 256;
+  size_t lds_max = 65536;  // dynamic + static LDS bytes one workgroup may use
   void* d_stage = nullptr;
   size_t stage_bytes = 0;
   std::string err;
@@ -345,6 +348,7 @@ prism_hip_ctx* prism_hip_ctx_create(int device) {
   auto* ctx = new prism_hip_ctx;
   ctx->device = device;
   ctx->num_cu = prop.multiProcessorCount;
+  ctx->lds_max = prop.sharedMemPerBlock;
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
     g_create_err = std::string("hipStreamCreate: ") + hipGetErrorString(e);
     delete ctx;
@@ -578,4 +582,90 @@ int prism_hip_lut_embed(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t 
 }  // extern "C"
 
 // GPU-resident decode step (prism_hip_model_*).
+
+// ---- palette compiler
+size_t prism_hip_palettize_bytes(uint32_t out_dim, uint32_t in_dim) {
+  return (size_t)out_dim * 32 + (size_t)out_dim * ((in_dim + 1) / 2);
+}
+
+static int check_palettize(prism_hip_ctx* ctx, uint32_t k) {
+  if (k == 0 || k > (uint32_t)prism::kPaletteMaxK)
+    return fail(ctx, PRISM_HIP_ERR_SHAPE, "palette size k=%u outside 1..%d (4-bit indices)", k, prism::kPaletteMaxK);
+  return PRISM_HIP_OK;
+}
+
+// Rows run one wave each.  When a row's values and scratch fit the
+// workgroup's LDS they live there; longer rows read values from d_w and keep
+// their scratch in a stream-ordered workspace of at most kWsBytes per launch.
+static int launch_palettize(prism_hip_ctx* ctx, const float* d_w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
+                            uint32_t max_iter, uint8_t* d_payload, hipStream_t st) {
+  constexpr uint32_t kMaxGrid = 1u << 20;
+  constexpr size_t kWsBytes = (size_t)256 << 20;
+  uint8_t* lut = d_payload;
+  uint8_t* idx = d_payload + (size_t)out_dim * 32;
+  const size_t lds = prism::palette_lds_bytes(in_dim);
+  const size_t stat = 3 * prism::kPaletteMaxK * 4;
+  if (lds + stat <= ctx->lds_max) {
+    for (uint32_t r0 = 0; r0 < out_dim; r0 += kMaxGrid) {
+      const uint32_t rows = std::min(kMaxGrid, out_dim - r0);
+      hipLaunchKernelGGL(prism::k_palettize<true>, dim3(rows), dim3(64), lds, st, d_w, in_dim, k, max_iter, r0,
+                         nullptr, lut, idx);
+      HIP_TRY(ctx, hipGetLastError());
+    }
+    return PRISM_HIP_OK;
+  }
+  const uint32_t chunk = (uint32_t)std::min<size_t>(kMaxGrid, std::max<size_t>(1, kWsBytes / ((size_t)in_dim * 4)));
+  const size_t wsb = (size_t)std::min(chunk, out_dim) * in_dim * 4;
+  void* ws = nullptr;
+  HIP_TRY(ctx, hipMallocAsync(&ws, wsb, st));
+  for (uint32_t r0 = 0; r0 < out_dim; r0 += chunk) {
+    const uint32_t rows = std::min(chunk, out_dim - r0);
+    hipLaunchKernelGGL(prism::k_palettize<false>, dim3(rows), dim3(64), 0, st, d_w, in_dim, k, max_iter, r0,
+                       reinterpret_cast<float*>(ws), lut, idx);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+      (void)hipFreeAsync(ws, st);
+      return fail(ctx, PRISM_HIP_ERR_DEVICE, "k_palettize launch failed: %s", hipGetErrorString(e));
+    }
+  }
+  HIP_TRY(ctx, hipFreeAsync(ws, st));
+  return PRISM_HIP_OK;
+}
+
+int prism_hip_palettize(prism_hip_ctx* ctx, const float* w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
+                        uint32_t max_iter, uint8_t* payload) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_palettize(ctx, k);
+  if (rc) return rc;
+  if (out_dim == 0) return PRISM_HIP_OK;
+  if (!payload || (!w && in_dim)) return fail(ctx, PRISM_HIP_ERR_NULL, "weights or payload is NULL");
+  DeviceGuard g(ctx->device);
+  const size_t wb = (size_t)out_dim * in_dim * 4, pb = prism_hip_palettize_bytes(out_dim, in_dim);
+  const size_t poff = (wb + 255) & ~(size_t)255;
+  if ((rc = ensure_stage(ctx, poff + pb))) return rc;
+  uint8_t* st = reinterpret_cast<uint8_t*>(ctx->d_stage);
+  if (wb) HIP_TRY(ctx, hipMemcpyAsync(st, w, wb, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = launch_palettize(ctx, reinterpret_cast<const float*>(st), out_dim, in_dim, k, max_iter, st + poff,
+                             ctx->stream)))
+    return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(payload, st + poff, pb, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+int prism_hip_palettize_dev(prism_hip_ctx* ctx, const void* d_w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
+                            uint32_t max_iter, void* d_payload, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_palettize(ctx, k);
+  if (rc) return rc;
+  if (out_dim == 0) return PRISM_HIP_OK;
+  if (!d_payload || (!d_w && in_dim)) return fail(ctx, PRISM_HIP_ERR_NULL, "weights or payload is NULL");
+  DeviceGuard g(ctx->device);
+  rc = launch_palettize(ctx, reinterpret_cast<const float*>(d_w), out_dim, in_dim, k, max_iter,
+                        reinterpret_cast<uint8_t*>(d_payload), pick_stream(ctx, stream));
+  if (rc == PRISM_HIP_OK) ctx->err.clear();
+  return rc;
+}
+
 #include "model_step.hpp"

@@ -1,0 +1,251 @@
+"""Pinning of the palette-compiler oracle (oracle/prism_cpuref_palette.c).
+
+The oracle restates fit_palette / encode_channel / palettize_matrix
+(src/quantization/palette.rs:75-272) and compile_to_cimage's payload
+assembly (src/lut/compiler.rs:47-60).  It is pinned here by
+
+* the reference's own known-answer tests (palette.rs:373-523);
+* exact integer arithmetic: on small-integer channels every fp32 distance,
+  total and cumulative sum of the k-means++ initialization and every
+  cluster sum of the first Lloyd step is exact, so the centroids those steps
+  must produce follow from Python integers (only the threshold product and
+  the mean's division round, once each, both computed here with numpy's
+  IEEE float32);
+* closed forms: k = n distinct values gives the channel itself sorted by
+  magnitude; a channel with at most k distinct values is reproduced exactly;
+* a vectorised numpy argmin for the encoder.
+"""
+import importlib
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+
+pe = importlib.import_module("prism-engine_amd")
+
+
+def decode(payload, rows, cols):
+    """dequantize_matrix (palette.rs) over the compiled payload: every
+    element through its row's fp16 LUT, rows (cols+1)/2 bytes apart."""
+    rb = (cols + 1) // 2
+    lut = payload[:rows * 32].view(np.float16).reshape(rows, 16).astype(np.float32)
+    idx = pe.palette.unpack_nibbles(payload[rows * 32:].reshape(rows, rb), cols)
+    return np.take_along_axis(lut, idx.astype(np.int64), axis=1)
+
+
+# ---- reference known-answer tests (palette.rs:373-523) ----------------------
+
+def test_fit_palette_three_clusters_kat():
+    # palette.rs:373-408: clusters at -5, 0, 5 -> centroids near them.
+    data = [-5.0] * 5 + [0.0] * 5 + [5.0] * 5
+    cb = oracle.fit_palette(data, 3, 50)
+    assert cb.size == 3
+    s = np.sort(cb)
+    assert abs(s[0] + 5) < 0.1 and abs(s[1]) < 0.1 and abs(s[2] - 5) < 0.1
+    # exact: |5| == |-5| keeps the init order (5 was picked first), 0 last
+    assert cb.tolist() == [5.0, -5.0, 0.0]
+
+
+def test_encode_channel_kat():
+    # palette.rs:410-425
+    packed, mse = oracle.encode_channel([1.0, 2.0, 3.0, 4.0], [1.0, 2.0, 3.0, 4.0] + [0.0] * 12)
+    assert packed.tolist() == [0x10, 0x32]
+    assert mse < 0.001 and mse == 0.0
+
+
+def test_palettize_matrix_roundtrip_kat():
+    # palette.rs:427-459: 3x4, k=4 -> 2 index bytes per row, 4 non-zero entries, MSE < 2
+    w = np.arange(1, 13, dtype=np.float32).reshape(3, 4)
+    payload, mse = oracle.palettize_payload(w, 4, 50)
+    assert payload.size == 3 * 32 + 3 * 2
+    lut = payload[:96].view(np.float16).reshape(3, 16).astype(np.float32)
+    assert np.all(lut[:, :4] != 0) and np.all(lut[:, 4:] == 0)
+    dec = decode(payload, 3, 4)
+    assert np.mean((dec - w) ** 2) < 2.0
+    assert np.array_equal(dec, w)  # four distinct values per row, k = 4: exact
+    assert np.all(mse == 0)
+
+
+def test_palettize_large_random_kat():
+    # palette.rs:461-492: 64x128 sin data, k=16, 30 iterations
+    w = np.sin(np.arange(8192, dtype=np.float32) / np.float32(8192.0) * np.float32(10.0)
+               - np.float32(5.0)).astype(np.float32).reshape(64, 128)
+    payload, mse = oracle.palettize_payload(w, 16, 30)
+    bpp = (64 * 128 * 4 + 64 * 16 * 16) / (64 * 128)  # effective_bpp (palette.rs:48-61)
+    assert 4.0 < bpp < 10.0
+    dec = decode(payload, 64, 128)
+    full = float(np.mean((dec - w) ** 2))
+    assert full < 5.0
+    # the per-row encode MSE (f32 codebook) agrees with the decoded error up
+    # to the fp16 rounding of the LUT
+    assert abs(float(np.mean(mse)) - full) < 1e-5
+
+
+def test_empty_channel_kat():
+    # palette.rs:495-499
+    assert oracle.fit_palette([], 16, 50).size == 0
+
+
+def test_single_value_kat():
+    # palette.rs:501-523
+    data = [42.0] * 100
+    cb = oracle.fit_palette(data, 4, 50)
+    assert cb.tolist() == [42.0] * 4
+    packed, mse = oracle.encode_channel(data, cb)
+    assert mse < 0.01 and np.all(packed == 0)
+
+
+# ---- exact integer arithmetic ----------------------------------------------
+
+def _frac(seed):
+    x = seed * 0.6180339887498949
+    return x - math.trunc(x)
+
+
+def _init_exact(ch, k):
+    """k-means++ picks on an integer channel, in exact integer arithmetic."""
+    n = len(ch)
+    k = min(k, n)
+    c = [ch[n // 2]]
+    md = [None] * n
+    for nc in range(1, k):
+        last = c[-1]
+        for i, v in enumerate(ch):
+            d = (v - last) ** 2
+            md[i] = d if md[i] is None else min(md[i], d)
+        total = sum(md)
+        assert total < 2 ** 24  # every fp32 partial sum is exact
+        if total <= 0:
+            c.append(ch[(nc * n // k) % n])
+            continue
+        target = float(np.float32(total) * np.float32(_frac(nc)))
+        cum, picked = 0, 0
+        for i, d in enumerate(md):
+            cum += d
+            if cum >= target:
+                picked = i
+                break
+        c.append(ch[picked])
+    return c
+
+
+def _lloyd1_exact(ch, c):
+    """One Lloyd step: first strictly nearest centroid, integer sums, one
+    IEEE float32 division per cluster."""
+    k = len(c)
+    sums, counts = [0] * k, [0] * k
+    for v in ch:
+        dists = [(v - cj) ** 2 for cj in c]
+        j = dists.index(min(dists))  # first minimum
+        sums[j] += v
+        counts[j] += 1
+    return [float(np.float32(sums[j]) / np.float32(counts[j])) if counts[j] else float(c[j]) for j in range(k)]
+
+
+def _by_magnitude(c):
+    return sorted(c, key=lambda v: -abs(v))  # stable, like sort_by
+
+
+@pytest.mark.parametrize("seed,n,k", [(1, 37, 16), (2, 200, 16), (3, 1000, 16), (4, 15, 4), (5, 64, 7),
+                                      (6, 1999, 16), (7, 9, 16)])
+def test_init_matches_exact_integer_picks(seed, n, k):
+    rng = np.random.default_rng(seed)
+    ch = rng.integers(-40, 41, n).tolist()
+    want = _by_magnitude([float(v) for v in _init_exact(ch, k)])
+    got = oracle.fit_palette(np.array(ch, np.float32), k, 0).tolist()  # max_iter 0: init only
+    assert got == want
+
+
+@pytest.mark.parametrize("seed,n,k", [(11, 50, 16), (12, 300, 16), (13, 1200, 16), (14, 80, 5)])
+def test_one_lloyd_step_matches_exact(seed, n, k):
+    rng = np.random.default_rng(seed)
+    ch = rng.integers(-40, 41, n).tolist()
+    want = _by_magnitude(_lloyd1_exact(ch, _init_exact(ch, k)))
+    got = oracle.fit_palette(np.array(ch, np.float32), k, 1).tolist()
+    assert got == want
+
+
+def test_init_threshold_fallback_when_total_is_zero():
+    # two distinct values, k = 6: after both are picked the total is 0 and
+    # the remaining picks are ch[(nc * n / k) % n]
+    ch = [3] * 10 + [-7] * 2
+    want = _by_magnitude([float(v) for v in _init_exact(ch, 6)])
+    assert oracle.fit_palette(np.array(ch, np.float32), 6, 0).tolist() == want
+    assert sorted(set(want)) == [-7.0, 3.0]
+
+
+# ---- closed forms -----------------------------------------------------------
+
+@pytest.mark.parametrize("seed,n", [(21, 16), (22, 9), (23, 2), (24, 1)])
+def test_k_equals_n_distinct_gives_sorted_channel(seed, n):
+    """Every k-means++ pick lands on an element at positive distance, so with
+    k = n distinct values the palette is the channel itself; each element is
+    its own cluster and Lloyd leaves it in place."""
+    rng = np.random.default_rng(seed)
+    ch = rng.standard_normal(n).astype(np.float32)
+    if n > 1:
+        ch[0] = -ch[1]  # a magnitude tie with opposite signs
+    cb = oracle.fit_palette(ch, n, 50)
+    assert sorted(cb.tolist()) == sorted(ch.tolist())
+    mags = np.abs(cb)
+    assert np.all(mags[:-1] >= mags[1:])
+    packed, mse = oracle.encode_channel(ch, cb)
+    assert mse == 0.0
+    idx = pe.palette.unpack_nibbles(packed[None, :], n)[0]
+    assert np.array_equal(cb[idx], ch)
+
+
+@pytest.mark.parametrize("seed,rows,cols,distinct", [(31, 8, 256, 16), (32, 5, 97, 3), (33, 3, 16, 16),
+                                                     (34, 6, 1000, 11)])
+def test_few_distinct_values_are_reproduced_exactly(seed, rows, cols, distinct):
+    """A row drawn from at most 16 fp16 values compiles to a payload that
+    decodes to those values exactly (compile -> decode round trip)."""
+    rng = np.random.default_rng(seed)
+    vals = (rng.standard_normal((rows, distinct)) * 0.05).astype(np.float16).astype(np.float32)
+    w = np.take_along_axis(vals, rng.integers(0, distinct, (rows, cols)), axis=1)
+    payload, mse = oracle.palettize_payload(w, 16, 50)
+    assert np.array_equal(decode(payload, rows, cols), w)
+    assert np.all(mse == 0)
+
+
+# ---- encoder against numpy --------------------------------------------------
+
+@pytest.mark.parametrize("seed,n,kc", [(41, 1000, 16), (42, 33, 5), (43, 4096, 16), (44, 7, 1)])
+def test_encode_channel_matches_numpy_argmin(seed, n, kc):
+    rng = np.random.default_rng(seed)
+    ch = rng.standard_normal(n).astype(np.float32)
+    cb = rng.standard_normal(kc).astype(np.float32)
+    cb[-1] = cb[0]  # duplicate entry: the first one wins
+    packed, mse = oracle.encode_channel(ch, cb)
+    d = (ch[:, None] - cb[None, :]) ** 2
+    idx = np.argmin(d, axis=1)  # first minimum
+    assert np.array_equal(packed, pe.palette.pack_nibbles(idx[None, :].astype(np.uint8))[0])
+    assert abs(mse - float(np.mean(d.min(axis=1).astype(np.float64)))) <= 1e-5 * max(1.0, mse)
+
+
+# ---- payload assembly (compiler.rs:47-60) -----------------------------------
+
+def test_payload_is_lut_block_then_index_block():
+    rng = np.random.default_rng(51)
+    w = rng.standard_normal((5, 21)).astype(np.float32)  # odd in_dim: 11 bytes per row
+    payload, mse = oracle.palettize_payload(w, 16, 50)
+    rb = 11
+    assert payload.size == 5 * 32 + 5 * rb
+    for r in range(5):
+        cb = oracle.fit_palette(w[r], 16, 50)
+        lut = np.zeros(16, np.float32)
+        lut[:cb.size] = cb
+        assert np.array_equal(payload[r * 32:(r + 1) * 32], lut.astype(np.float16).view(np.uint8))
+        packed, e = oracle.encode_channel(w[r], cb)
+        assert np.array_equal(payload[160 + r * rb:160 + (r + 1) * rb], packed)
+        assert e == mse[r]
+
+
+def test_threaded_payload_is_identical():
+    rng = np.random.default_rng(52)
+    w = (rng.standard_normal((64, 96)) * 0.02).astype(np.float32)
+    a, ea = oracle.palettize_payload(w, 16, 50, threads=1)
+    b, eb = oracle.palettize_payload(w, 16, 50, threads=4)
+    assert np.array_equal(a, b) and np.array_equal(ea, eb)
