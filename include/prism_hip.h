@@ -146,12 +146,19 @@ int prism_hip_decode_rows_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, uin
  * threshold of :186-191, encode_channel :198-228) plus compile_to_cimage's
  * payload assembly (src/lut/compiler.rs:47-60, called with k=16,
  * max_iter=50); the payload is byte-identical to the reference's.
- * k must be 1..16 (PRISM_HIP_ERR_SHAPE otherwise). */
+ * k must be 1..16 (PRISM_HIP_ERR_SHAPE otherwise).  seeds (host memory, may
+ * be NULL) are the calibration seeds of compute-core's
+ * palettize_matrix_phased (compute-core/src/quantization/palette.rs:
+ * 94-116, 409-431): the first min(nseeds, k) centroids of every row, with
+ * k-means++ continuing from them; NULL starts every row from channel[n/2]
+ * as the root crate does.  Non-NULL seeds need nseeds >= 1 (the reference
+ * panics on an empty list); entries past 16 are never used. */
 size_t prism_hip_palettize_bytes(uint32_t out_dim, uint32_t in_dim);
 int prism_hip_palettize(prism_hip_ctx* ctx, const float* w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
-                        uint32_t max_iter, uint8_t* payload);
+                        uint32_t max_iter, const float* seeds, uint32_t nseeds, uint8_t* payload);
 int prism_hip_palettize_dev(prism_hip_ctx* ctx, const void* d_w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
-                            uint32_t max_iter, void* d_payload, void* stream);
+                            uint32_t max_iter, const float* seeds, uint32_t nseeds, void* d_payload,
+                            void* stream);
 
 /* ---- keyed backend (MetalBackend's surface) ------------------------------ */
 

@@ -43,11 +43,17 @@ palettize_matrix and compile_to_cimage's payload):
 * ``encode_channel``: KAT palette.rs:410-425 (0x10, 0x32, MSE 0), brute-force
   argmin over the codebook on random data -- pinned.
 * ``fit_palette``: KATs palette.rs:373-408 (three clusters), :495-523 (empty,
-  constant channel); invariants (sorted by magnitude, fixed point of one Lloyd
-  step when converged, k = min(k, n)); a numpy restatement of the k-means++
-  pick on small inputs -- pinned.
+  constant channel); exact integer arithmetic on small-integer channels (the
+  k-means++ picks, the zero-total fallback and one Lloyd step follow from
+  Python integers); closed forms (k = n distinct values gives the channel
+  sorted by magnitude; at most k distinct values are reproduced exactly)
+  -- pinned.
 * ``palettize_payload``: KATs palette.rs:427-492 (3x4 round trip, 64x128 MSE
   bound), layout of compiler.rs:47-60 -- pinned.
+* seeded variant (compute-core's palettize_matrix_phased seeds): closed
+  forms (k distinct seeds reproduce themselves; seeds that hit every value
+  give an exact payload) and exact-integer picks continuing from the last
+  seed -- pinned.
 """
 from __future__ import annotations
 
@@ -136,6 +142,12 @@ def lib():
         L.cpuref_palettize_payload.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
                                                ctypes.c_size_t, _u8p, _f32p]
         L.cpuref_palettize_payload.restype = ctypes.c_int
+        L.cpuref_fit_palette_seeded.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _f32p,
+                                                ctypes.c_size_t, _f32p]
+        L.cpuref_fit_palette_seeded.restype = ctypes.c_size_t
+        L.cpuref_palettize_payload_seeded.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                                      ctypes.c_size_t, _f32p, ctypes.c_size_t, _u8p, _f32p]
+        L.cpuref_palettize_payload_seeded.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -376,12 +388,22 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
-def fit_palette(channel, k: int = 16, max_iter: int = 50) -> np.ndarray:
-    """fit_palette (palette.rs:75-183): min(k, n) centroids, |c| descending."""
+def fit_palette(channel, k: int = 16, max_iter: int = 50, seeds=None) -> np.ndarray:
+    """fit_palette (palette.rs:75-183): min(k, n) centroids, |c| descending.
+    seeds: compute-core's seeded variant (compute-core/src/quantization/
+    palette.rs:94-201), the first min(len, k) centroids."""
     ch = _f32(channel)
     out = np.zeros(max(k, 1), dtype=np.float32)
-    kc = lib().cpuref_fit_palette(ch.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), ch.size, k, max_iter,
-                                  out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    fp = ctypes.POINTER(ctypes.c_float)
+    if seeds is None:
+        sp, ns = None, 0
+    else:
+        sd = _f32(seeds)
+        if sd.size == 0:
+            raise ValueError("empty seed list (the reference indexes centroids[-1])")
+        sp, ns = sd.ctypes.data_as(fp), sd.size
+    kc = lib().cpuref_fit_palette_seeded(ch.ctypes.data_as(fp), ch.size, k, max_iter, sp, ns,
+                                         out.ctypes.data_as(fp))
     return out[:kc].copy()
 
 
@@ -395,27 +417,33 @@ def encode_channel(channel, codebook):
     return packed, float(mse)
 
 
-def palettize_payload(weights, k: int = 16, max_iter: int = 50, threads: int = 1):
+def palettize_payload(weights, k: int = 16, max_iter: int = 50, threads: int = 1, seeds=None):
     """palettize_matrix + compile_to_cimage's payload (compiler.rs:47-60) for a
-    [out_dim, in_dim] f32 matrix: (payload bytes, per-row MSE)."""
+    [out_dim, in_dim] f32 matrix: (payload bytes, per-row MSE).  seeds: the
+    calibration seeds of compute-core's palettize_matrix_phased, shared by
+    every row."""
     w = _f32(weights)
     assert w.ndim == 2
     out_dim, in_dim = w.shape
     payload = np.zeros(out_dim * 32 + out_dim * ((in_dim + 1) // 2), dtype=np.uint8)
     mse = np.zeros(out_dim, dtype=np.float32)
     fp = ctypes.POINTER(ctypes.c_float)
+    sd = None if seeds is None else _f32(seeds)
+    if sd is not None and sd.size == 0:
+        raise ValueError("empty seed list (the reference indexes centroids[-1])")
     if threads <= 1 or out_dim < 2 * threads:
-        rc = lib().cpuref_palettize_payload(w.ctypes.data_as(fp), out_dim, in_dim, k, max_iter, _p8(payload),
-                                            mse.ctypes.data_as(fp))
+        rc = lib().cpuref_palettize_payload_seeded(w.ctypes.data_as(fp), out_dim, in_dim, k, max_iter,
+                                                   None if sd is None else sd.ctypes.data_as(fp),
+                                                   0 if sd is None else sd.size, _p8(payload),
+                                                   mse.ctypes.data_as(fp))
         assert rc == 0
         return payload, mse
     # rows are independent: split them over host threads (identical bytes)
     from concurrent.futures import ThreadPoolExecutor
     bounds = np.linspace(0, out_dim, threads + 1).astype(int)
-    parts = []
 
     def run(a, b):
-        p, e = palettize_payload(w[a:b], k, max_iter, 1)
+        p, e = palettize_payload(w[a:b], k, max_iter, 1, sd)
         return a, b, p, e
 
     with ThreadPoolExecutor(threads) as ex:

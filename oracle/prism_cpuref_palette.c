@@ -9,7 +9,15 @@
  *                             (k-means++ init from channel[n/2] with the
  *                             golden-ratio threshold of :186-191, Lloyd
  *                             iterations with a 0.001 shift exit, centroids
- *                             sorted by magnitude, descending, stably)
+ *                             sorted by magnitude, descending, stably).
+ *                             With seeds: compute-core's fit_palette
+ *                             (compute-core/src/quantization/palette.rs:
+ *                             94-201): the first min(len, k) centroids are
+ *                             the seeds and k-means++ continues from them
+ *                             (its first distance pass sees only the last
+ *                             seed, as there); the rest is unchanged (its
+ *                             transposed assignment loop picks the same
+ *                             first strictly nearest centroid).
  *   cpuref_encode_channel     encode_channel, palette.rs:198-228
  *   cpuref_palettize_payload  palettize_matrix (palette.rs:230-272) followed
  *                             by compile_to_cimage's payload assembly
@@ -33,13 +41,20 @@ static float weighted_threshold(float total, size_t seed) {
   return total * (float)frac;
 }
 
-/* Returns the number of centroids written to out (min(k, n); 0 for n == 0). */
-size_t cpuref_fit_palette(const float* ch, size_t n, size_t k, size_t max_iter, float* out) {
+/* Returns the number of centroids written to out (min(k, n); 0 for n == 0).
+ * seeds may be NULL (root crate fit_palette); otherwise nseeds >= 1. */
+size_t cpuref_fit_palette_seeded(const float* ch, size_t n, size_t k, size_t max_iter, const float* seeds,
+                                 size_t nseeds, float* out) {
   if (n == 0 || k == 0) return 0;
+  if (seeds && nseeds == 0) return 0; /* the reference panics (centroids[-1]); callers reject it */
   if (k > n) k = n;
   float* c = out;
   size_t nc = 0;
-  c[nc++] = ch[n / 2];
+  if (seeds) {
+    for (size_t j = 0; j < nseeds && j < k; j++) c[nc++] = seeds[j];
+  } else {
+    c[nc++] = ch[n / 2];
+  }
   float* min_d = (float*)malloc(sizeof(float) * n);
   size_t* asg = (size_t*)malloc(sizeof(size_t) * n);
   for (size_t i = 0; i < n; i++) min_d[i] = 3.40282347e38f; /* f32::MAX */
@@ -119,6 +134,10 @@ size_t cpuref_fit_palette(const float* ch, size_t n, size_t k, size_t max_iter, 
   return k;
 }
 
+size_t cpuref_fit_palette(const float* ch, size_t n, size_t k, size_t max_iter, float* out) {
+  return cpuref_fit_palette_seeded(ch, n, k, max_iter, NULL, 0, out);
+}
+
 /* Packs (n+1)/2 bytes into packed (element 2i low nibble); returns the MSE. */
 float cpuref_encode_channel(const float* ch, size_t n, const float* cb, size_t kc, uint8_t* packed) {
   float mse = 0.0f;
@@ -147,14 +166,15 @@ float cpuref_encode_channel(const float* ch, size_t n, const float* cb, size_t k
 /* The compiler's split-block payload for a [out_dim x in_dim] f32 matrix:
  * out_dim*32 LUT bytes then out_dim*((in_dim+1)/2) index bytes.  mse (may be
  * NULL) receives each row's encode MSE. */
-int cpuref_palettize_payload(const float* w, size_t out_dim, size_t in_dim, size_t k, size_t max_iter,
-                             uint8_t* payload, float* mse) {
+int cpuref_palettize_payload_seeded(const float* w, size_t out_dim, size_t in_dim, size_t k, size_t max_iter,
+                                    const float* seeds, size_t nseeds, uint8_t* payload, float* mse) {
   if (k == 0 || k > 16) return -1;
+  if (seeds && nseeds == 0) return -1; /* the reference indexes centroids[-1] */
   const size_t rb = (in_dim + 1) / 2;
   uint8_t* idx = payload + out_dim * 32;
   for (size_t r = 0; r < out_dim; r++) {
     float cb[16] = {0};
-    const size_t kc = cpuref_fit_palette(w + r * in_dim, in_dim, k, max_iter, cb);
+    const size_t kc = cpuref_fit_palette_seeded(w + r * in_dim, in_dim, k, max_iter, seeds, nseeds, cb);
     const float e = cpuref_encode_channel(w + r * in_dim, in_dim, cb, kc, idx + r * rb);
     if (mse) mse[r] = e;
     for (size_t j = 0; j < 16; j++) {
@@ -164,4 +184,9 @@ int cpuref_palettize_payload(const float* w, size_t out_dim, size_t in_dim, size
     }
   }
   return 0;
+}
+
+int cpuref_palettize_payload(const float* w, size_t out_dim, size_t in_dim, size_t k, size_t max_iter,
+                             uint8_t* payload, float* mse) {
+  return cpuref_palettize_payload_seeded(w, out_dim, in_dim, k, max_iter, NULL, 0, payload, mse);
 }

@@ -66,9 +66,10 @@ SIGNATURES = {
     "prism_hip_lut_embed": (_c.c_int, [_vp, _vp, _c.c_uint32, _vp]),
     "prism_hip_decode_rows_dev": (_c.c_int, [_vp, _vp, _c.c_uint32, _c.c_uint32, _vp, _vp]),
     "prism_hip_palettize_bytes": (_c.c_size_t, [_c.c_uint32, _c.c_uint32]),
-    "prism_hip_palettize": (_c.c_int, [_vp, _vp, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_uint32, _vp]),
+    "prism_hip_palettize": (_c.c_int, [_vp, _vp, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_uint32, _vp,
+                                       _c.c_uint32, _vp]),
     "prism_hip_palettize_dev": (_c.c_int, [_vp, _vp, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_uint32, _vp,
-                                           _vp]),
+                                           _c.c_uint32, _vp, _vp]),
     "prism_hip_backend_new": (_vp, [_c.c_int]),
     "prism_hip_backend_free": (None, [_vp]),
     "prism_hip_backend_last_error": (_c.c_char_p, [_vp]),

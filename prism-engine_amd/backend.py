@@ -120,21 +120,31 @@ class Context:
     def palettize_bytes(self, out_dim: int, in_dim: int) -> int:
         return int(self.lib.prism_hip_palettize_bytes(out_dim, in_dim))
 
-    def palettize(self, w, k: int = 16, max_iter: int = 50) -> np.ndarray:
+    @staticmethod
+    def _seeds(seeds):
+        if seeds is None:
+            return None, None, 0
+        s = np.ascontiguousarray(seeds, dtype=np.float32).reshape(-1)
+        return s, s.ctypes.data, s.size
+
+    def palettize(self, w, k: int = 16, max_iter: int = 50, seeds=None) -> np.ndarray:
         """fp32 [out_dim, in_dim] weights -> the split-block payload (uint8),
-        byte-identical to the reference compiler's (k=16, max_iter=50 there)."""
+        byte-identical to the reference compiler's (k=16, max_iter=50 there).
+        seeds: compute-core's calibration seeds (first centroids of every row)."""
         w = np.ascontiguousarray(w, dtype=np.float32)
         if w.ndim != 2:
             raise ValueError(f"weights must be 2-D [out_dim, in_dim], got shape {w.shape}")
         out_dim, in_dim = w.shape
         out = np.empty(self.palettize_bytes(out_dim, in_dim), dtype=np.uint8)
+        keep, sp, ns = self._seeds(seeds)
         self.check(self.lib.prism_hip_palettize(self.h, w.ctypes.data if w.size else None, out_dim, in_dim, k,
-                                                max_iter, out.ctypes.data))
+                                                max_iter, sp, ns, out.ctypes.data))
         return out
 
     def palettize_dev(self, d_w, out_dim: int, in_dim: int, d_payload, k: int = 16, max_iter: int = 50,
-                      stream=None) -> None:
-        self.check(self.lib.prism_hip_palettize_dev(self.h, ptr(d_w), out_dim, in_dim, k, max_iter,
+                      stream=None, seeds=None) -> None:
+        keep, sp, ns = self._seeds(seeds)
+        self.check(self.lib.prism_hip_palettize_dev(self.h, ptr(d_w), out_dim, in_dim, k, max_iter, sp, ns,
                                                     ptr(d_payload), _stream_handle(stream)))
 
     def close(self) -> None:

@@ -7,14 +7,16 @@
 // 16 fp16 LUT entries (zero past k), then every row's packed indices,
 // (n+1)/2 bytes per row.
 //
-// One wave per row; the row and its scratch live in LDS.  The result is the
-// reference's byte for byte: every fp32 operation happens in the
-// reference's order where the order changes the result, and in parallel
-// only where it cannot:
+// One wave per row; the row and its scratch live in LDS (or, for rows too
+// long for LDS, in a global workspace).  The result is the reference's byte
+// for byte: every fp32 operation happens in the reference's order where the
+// order changes the result, and in parallel only where it cannot:
 //  * k-means++ picks (from channel[n/2], golden-ratio thresholds): the
-//    min-distance update is per element (parallel over lanes); the total and
-//    the cumulative scan that picks the next centroid are sequential fp32
-//    folds in element order (lane 0);
+//    min-distance update is per element (parallel over lanes); the total is
+//    a sequential fp32 fold in element order (lane 0) that also stores every
+//    partial sum; those partial sums are the reference's cumulative scan, and
+//    since they never decrease (non-negative terms, monotone rounding) the
+//    first one >= the threshold is found by binary search;
 //  * Lloyd iterations: the assignment (first strictly smallest squared
 //    distance) is per element (parallel); the per-cluster sums are
 //    sequential folds in element order, one lane per cluster, adding +0.0
@@ -23,6 +25,9 @@
 //    centroid moved by 0.001 or more;
 //  * a stable sort by magnitude, descending; encoding (first strictly
 //    nearest entry) per element; fp16 by RNE.
+// Arrays are padded to 16 elements (zeros; assignment 0xFF) so the
+// sequential folds read whole 16-element blocks; padding adds +0.0 and
+// belongs to no cluster.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -33,21 +38,86 @@ namespace prism {
 
 constexpr int kPaletteMaxK = 16;
 
-// Dynamic LDS bytes of the LDS-resident variant for rows of n elements:
-// values, then min-distances (initialization) reused as byte assignments
-// (Lloyd iterations).
-__host__ __device__ constexpr size_t palette_lds_bytes(uint32_t n) { return (size_t)n * 8; }
+// Calibration seeds (compute-core/src/quantization/palette.rs:94-116): the
+// first min(n, k) centroids of every row; n == 0 starts from channel[n/2]
+// (the root crate's fit_palette).
+struct PaletteSeeds {
+  float v[kPaletteMaxK];
+  uint32_t n;
+};
 
-// One wave per row r = row0 + blockIdx.x.  kLds: the row and its scratch in
-// LDS (palette_lds_bytes(n) dynamic bytes); otherwise values are read from w
-// and the scratch is ws[blockIdx.x * n ..] (n floats per row of the launch).
-// lut_out: 32 bytes per row (16 fp16 entries); idx_out: (n+1)/2 bytes per row.
+__host__ __device__ constexpr uint32_t palette_pad(uint32_t n) { return (n + 15u) & ~15u; }
+// Per row: values, min-distances (reused as byte assignments in the Lloyd
+// iterations) and partial sums, palette_pad(n) floats each.
+__host__ __device__ constexpr size_t palette_row_bytes(uint32_t n) { return (size_t)palette_pad(n) * 12; }
+
+// Sequential fp32 fold of v[0..np) (np % 16 == 0), storing each partial sum.
+__device__ __forceinline__ float palette_fold_prefix(const float* v, float* pre, uint32_t np) {
+  float s = 0.0f;
+  for (uint32_t i = 0; i < np; i += 16) {
+    float4 t[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) t[q] = reinterpret_cast<const float4*>(v + i)[q];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float4 o;
+      s += t[q].x;
+      o.x = s;
+      s += t[q].y;
+      o.y = s;
+      s += t[q].z;
+      o.z = s;
+      s += t[q].w;
+      o.w = s;
+      reinterpret_cast<float4*>(pre + i)[q] = o;
+    }
+  }
+  return s;
+}
+
+// Index of the first entry of the non-decreasing pre[0..n) that is >= t,
+// or 0 when there is none (the reference's pick when its scan runs out).
+__device__ __forceinline__ uint32_t palette_first_at_least(const float* pre, uint32_t n, float t) {
+  uint32_t lo = 0, hi = n;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (pre[mid] >= t)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo < n ? lo : 0u;
+}
+
+// First strictly nearest of the k (wave-uniform, <= 16) entries of c.
+__device__ __forceinline__ uint32_t palette_nearest(float v, const float (&c)[kPaletteMaxK], uint32_t k) {
+  float best = 3.40282347e38f;
+  uint32_t bi = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < (uint32_t)kPaletteMaxK; j++) {
+    if (j < k) {
+      const float dv = v - c[j];
+      const float d = dv * dv;
+      if (d < best) {
+        best = d;
+        bi = j;
+      }
+    }
+  }
+  return bi;
+}
+
+// Row r = row0 + blockIdx.x.  kLds: the row's arrays in LDS
+// (palette_row_bytes(n) dynamic bytes); otherwise in ws, palette_row_bytes(n)
+// bytes per row of the launch.  lut_out: 32 bytes per row (16 fp16 entries);
+// idx_out: (n+1)/2 bytes per row.
 template <bool kLds>
 __global__ __launch_bounds__(64) void k_palettize(const float* __restrict__ w, uint32_t n, uint32_t k,
-                                                  uint32_t max_iter, uint32_t row0, float* __restrict__ ws,
-                                                  uint8_t* __restrict__ lut_out, uint8_t* __restrict__ idx_out) {
+                                                  uint32_t max_iter, PaletteSeeds seeds, uint32_t row0,
+                                                  float* __restrict__ ws, uint8_t* __restrict__ lut_out,
+                                                  uint8_t* __restrict__ idx_out) {
 #pragma clang fp contract(off)
-  extern __shared__ float sm[];
+  extern __shared__ float4 sm4[];
   __shared__ float cent[kPaletteMaxK];
   __shared__ float s_new[kPaletteMaxK];
   __shared__ uint32_t s_moved[kPaletteMaxK];
@@ -58,80 +128,91 @@ __global__ __launch_bounds__(64) void k_palettize(const float* __restrict__ w, u
     if (lane < (uint32_t)kPaletteMaxK) lut[lane] = 0;
     return;
   }
+  const uint32_t np = palette_pad(n), nb4 = np / 4;
+  float* base = kLds ? reinterpret_cast<float*>(sm4) : ws + (size_t)blockIdx.x * (palette_row_bytes(n) / 4);
+  float* val = base;
+  float* md = base + np;
+  float* pre = base + 2 * (size_t)np;
+  uint32_t* asg4 = reinterpret_cast<uint32_t*>(md);  // 4 assignment bytes per word
   const float* row = w + (size_t)r * n;
   const float FMAX = 3.40282347e38f;  // f32::MAX
-  const float* val;
-  float* md;
-  if constexpr (kLds) {
-    float* v = sm;
-    md = sm + n;
-    for (uint32_t i = lane; i < n; i += 64) v[i] = row[i];
-    val = v;
-  } else {
-    val = row;
-    md = ws + (size_t)blockIdx.x * n;
+  for (uint32_t i = lane; i < np; i += 64) {
+    val[i] = i < n ? row[i] : 0.0f;
+    md[i] = i < n ? FMAX : 0.0f;  // padding stays at distance 0
   }
-  uint8_t* asg = reinterpret_cast<uint8_t*>(md);
-  for (uint32_t i = lane; i < n; i += 64) md[i] = FMAX;
   if (k > n) k = n;
-  if (lane == 0) cent[0] = row[n / 2];
+  const uint32_t ns = seeds.n < k ? seeds.n : k;
+  if (ns) {
+    if (lane < ns) cent[lane] = seeds.v[lane];
+  } else if (lane == 0) {
+    cent[0] = row[n / 2];
+  }
   __syncthreads();
 
-  // ---- k-means++ initialization
-  for (uint32_t nc = 1; nc < k; nc++) {
+  // ---- k-means++ initialization (its first pass sees only the last seed)
+  for (uint32_t nc = ns ? ns : 1; nc < k; nc++) {
     const float last = cent[nc - 1];
-    for (uint32_t i = lane; i < n; i += 64) {
-      const float dv = val[i] - last;
-      const float d = dv * dv;
-      if (d < md[i]) md[i] = d;
+    for (uint32_t b = lane; b < nb4; b += 64) {
+      const float4 v = reinterpret_cast<const float4*>(val)[b];
+      float4 m = reinterpret_cast<const float4*>(md)[b];
+      float dv = v.x - last, d = dv * dv;
+      if (d < m.x) m.x = d;
+      dv = v.y - last, d = dv * dv;
+      if (d < m.y) m.y = d;
+      dv = v.z - last, d = dv * dv;
+      if (d < m.z) m.z = d;
+      dv = v.w - last, d = dv * dv;
+      if (d < m.w) m.w = d;
+      reinterpret_cast<float4*>(md)[b] = m;
     }
     __syncthreads();
     if (lane == 0) {
-      float total = 0.0f;
-      for (uint32_t i = 0; i < n; i++) total += md[i];
+      const float total = palette_fold_prefix(md, pre, np);
+      uint32_t pick;
       if (total <= 0.0f) {
-        cent[nc] = val[(uint32_t)(((uint64_t)nc * n / k) % n)];
+        pick = (uint32_t)(((uint64_t)nc * n / k) % n);
       } else {
         const double x = (double)nc * 0.6180339887498949;
-        const float target = total * (float)(x - trunc(x));
-        float cum = 0.0f;
-        uint32_t picked = 0;
-        for (uint32_t i = 0; i < n; i++) {
-          cum += md[i];
-          if (cum >= target) {
-            picked = i;
-            break;
-          }
-        }
-        cent[nc] = val[picked];
+        pick = palette_first_at_least(pre, n, total * (float)(x - trunc(x)));
       }
+      cent[nc] = val[pick];
     }
     __syncthreads();
   }
 
   // ---- Lloyd iterations
+  float c[kPaletteMaxK];
   for (uint32_t it = 0; it < max_iter; it++) {
-    for (uint32_t i = lane; i < n; i += 64) {
-      float best = FMAX;
-      uint32_t bc = 0;
-      for (uint32_t j = 0; j < k; j++) {
-        const float dv = val[i] - cent[j];
-        const float d = dv * dv;
-        if (d < best) {
-          best = d;
-          bc = j;
-        }
-      }
-      asg[i] = (uint8_t)bc;
+#pragma unroll
+    for (int j = 0; j < kPaletteMaxK; j++) c[j] = cent[j];
+    for (uint32_t b = lane; b < nb4; b += 64) {
+      const float4 v = reinterpret_cast<const float4*>(val)[b];
+      uint32_t a = palette_nearest(v.x, c, k) | palette_nearest(v.y, c, k) << 8 |
+                   palette_nearest(v.z, c, k) << 16 | palette_nearest(v.w, c, k) << 24;
+      const uint32_t i0 = 4 * b;  // padding: no cluster
+      if (i0 + 4 > n) a |= 0xFFFFFFFFu << (8 * (n > i0 ? n - i0 : 0));
+      asg4[b] = a;
     }
     __syncthreads();
     if (lane < k) {
       float acc = 0.0f;
       uint32_t cnt = 0;
-      for (uint32_t i = 0; i < n; i++) {
-        const bool mine = asg[i] == lane;
-        acc += mine ? val[i] : 0.0f;
-        cnt += mine ? 1u : 0u;
+      for (uint32_t i = 0; i < np; i += 16) {
+        const uint4 a = *reinterpret_cast<const uint4*>(asg4 + i / 4);
+        float4 t[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) t[q] = reinterpret_cast<const float4*>(val + i)[q];
+        const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float tv[4] = {t[q].x, t[q].y, t[q].z, t[q].w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const bool mine = ((aw[q] >> (8 * e)) & 0xFFu) == lane;
+            acc += mine ? tv[e] : 0.0f;
+            cnt += mine ? 1u : 0u;
+          }
+        }
       }
       // 0: empty cluster (centroid kept); 1: updated; 2: updated and moved
       // by >= 0.001 (a NaN shift counts as not moved, like the max fold).
@@ -165,26 +246,16 @@ __global__ __launch_bounds__(64) void k_palettize(const float* __restrict__ w, u
   __syncthreads();
 
   // ---- LUT (fp16, zero past k) and packed indices
+#pragma unroll
+  for (int j = 0; j < kPaletteMaxK; j++) c[j] = cent[j];
   if (lane < (uint32_t)kPaletteMaxK) lut[lane] = f2h(lane < k ? cent[lane] : 0.0f);
   const uint32_t rb = (n + 1) / 2;
+  uint8_t* out = idx_out + (size_t)r * rb;
   for (uint32_t b = lane; b < rb; b += 64) {
-    uint32_t byte = 0;
-    for (uint32_t h = 0; h < 2; h++) {
-      const uint32_t i = 2 * b + h;
-      if (i >= n) break;
-      float best = FMAX;
-      uint32_t bi = 0;
-      for (uint32_t j = 0; j < k; j++) {
-        const float dv = val[i] - cent[j];
-        const float d = dv * dv;
-        if (d < best) {
-          best = d;
-          bi = j;
-        }
-      }
-      byte |= bi << (4 * h);
-    }
-    idx_out[(size_t)r * rb + b] = (uint8_t)byte;
+    const uint32_t i = 2 * b;
+    uint32_t byte = palette_nearest(val[i], c, k);
+    if (i + 1 < n) byte |= palette_nearest(val[i + 1], c, k) << 4;
+    out[b] = (uint8_t)byte;
   }
 }
 

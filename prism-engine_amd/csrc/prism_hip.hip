@@ -588,40 +588,49 @@ size_t prism_hip_palettize_bytes(uint32_t out_dim, uint32_t in_dim) {
   return (size_t)out_dim * 32 + (size_t)out_dim * ((in_dim + 1) / 2);
 }
 
-static int check_palettize(prism_hip_ctx* ctx, uint32_t k) {
+static int check_palettize(prism_hip_ctx* ctx, uint32_t k, const float* seeds, uint32_t nseeds,
+                           prism::PaletteSeeds* ps) {
   if (k == 0 || k > (uint32_t)prism::kPaletteMaxK)
     return fail(ctx, PRISM_HIP_ERR_SHAPE, "palette size k=%u outside 1..%d (4-bit indices)", k, prism::kPaletteMaxK);
+  *ps = prism::PaletteSeeds{};
+  if (seeds) {
+    if (nseeds == 0)  // the reference would index centroids[-1]
+      return fail(ctx, PRISM_HIP_ERR_SHAPE, "seeds given with nseeds = 0");
+    ps->n = std::min<uint32_t>(nseeds, prism::kPaletteMaxK);
+    std::memcpy(ps->v, seeds, ps->n * sizeof(float));
+  }
   return PRISM_HIP_OK;
 }
 
-// Rows run one wave each.  When a row's values and scratch fit the
-// workgroup's LDS they live there; longer rows read values from d_w and keep
-// their scratch in a stream-ordered workspace of at most kWsBytes per launch.
+// Rows run one wave each.  When a row's arrays fit the workgroup's LDS they
+// live there; longer rows keep them in a stream-ordered workspace of at most
+// kWsBytes per launch.
 static int launch_palettize(prism_hip_ctx* ctx, const float* d_w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
-                            uint32_t max_iter, uint8_t* d_payload, hipStream_t st) {
+                            uint32_t max_iter, const prism::PaletteSeeds& seeds, uint8_t* d_payload,
+                            hipStream_t st) {
   constexpr uint32_t kMaxGrid = 1u << 20;
   constexpr size_t kWsBytes = (size_t)256 << 20;
   uint8_t* lut = d_payload;
   uint8_t* idx = d_payload + (size_t)out_dim * 32;
-  const size_t lds = prism::palette_lds_bytes(in_dim);
+  const size_t lds = prism::palette_row_bytes(in_dim);
   const size_t stat = 3 * prism::kPaletteMaxK * 4;
   if (lds + stat <= ctx->lds_max) {
     for (uint32_t r0 = 0; r0 < out_dim; r0 += kMaxGrid) {
       const uint32_t rows = std::min(kMaxGrid, out_dim - r0);
-      hipLaunchKernelGGL(prism::k_palettize<true>, dim3(rows), dim3(64), lds, st, d_w, in_dim, k, max_iter, r0,
-                         nullptr, lut, idx);
+      hipLaunchKernelGGL(prism::k_palettize<true>, dim3(rows), dim3(64), lds, st, d_w, in_dim, k, max_iter, seeds,
+                         r0, nullptr, lut, idx);
       HIP_TRY(ctx, hipGetLastError());
     }
     return PRISM_HIP_OK;
   }
-  const uint32_t chunk = (uint32_t)std::min<size_t>(kMaxGrid, std::max<size_t>(1, kWsBytes / ((size_t)in_dim * 4)));
-  const size_t wsb = (size_t)std::min(chunk, out_dim) * in_dim * 4;
+  const uint32_t chunk = (uint32_t)std::min<size_t>(kMaxGrid, std::max<size_t>(1, kWsBytes / lds));
+  const size_t wsb = (size_t)std::min(chunk, out_dim) * lds;
   void* ws = nullptr;
   HIP_TRY(ctx, hipMallocAsync(&ws, wsb, st));
   for (uint32_t r0 = 0; r0 < out_dim; r0 += chunk) {
     const uint32_t rows = std::min(chunk, out_dim - r0);
-    hipLaunchKernelGGL(prism::k_palettize<false>, dim3(rows), dim3(64), 0, st, d_w, in_dim, k, max_iter, r0,
-                       reinterpret_cast<float*>(ws), lut, idx);
+    hipLaunchKernelGGL(prism::k_palettize<false>, dim3(rows), dim3(64), 0, st, d_w, in_dim, k, max_iter, seeds,
+                       r0, reinterpret_cast<float*>(ws), lut, idx);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
       (void)hipFreeAsync(ws, st);
@@ -633,9 +642,10 @@ static int launch_palettize(prism_hip_ctx* ctx, const float* d_w, uint32_t out_d
 }
 
 int prism_hip_palettize(prism_hip_ctx* ctx, const float* w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
-                        uint32_t max_iter, uint8_t* payload) {
+                        uint32_t max_iter, const float* seeds, uint32_t nseeds, uint8_t* payload) {
   if (!ctx) return PRISM_HIP_ERR_NULL;
-  int rc = check_palettize(ctx, k);
+  prism::PaletteSeeds ps;
+  int rc = check_palettize(ctx, k, seeds, nseeds, &ps);
   if (rc) return rc;
   if (out_dim == 0) return PRISM_HIP_OK;
   if (!payload || (!w && in_dim)) return fail(ctx, PRISM_HIP_ERR_NULL, "weights or payload is NULL");
@@ -645,7 +655,7 @@ int prism_hip_palettize(prism_hip_ctx* ctx, const float* w, uint32_t out_dim, ui
   if ((rc = ensure_stage(ctx, poff + pb))) return rc;
   uint8_t* st = reinterpret_cast<uint8_t*>(ctx->d_stage);
   if (wb) HIP_TRY(ctx, hipMemcpyAsync(st, w, wb, hipMemcpyHostToDevice, ctx->stream));
-  if ((rc = launch_palettize(ctx, reinterpret_cast<const float*>(st), out_dim, in_dim, k, max_iter, st + poff,
+  if ((rc = launch_palettize(ctx, reinterpret_cast<const float*>(st), out_dim, in_dim, k, max_iter, ps, st + poff,
                              ctx->stream)))
     return rc;
   HIP_TRY(ctx, hipMemcpyAsync(payload, st + poff, pb, hipMemcpyDeviceToHost, ctx->stream));
@@ -655,14 +665,15 @@ int prism_hip_palettize(prism_hip_ctx* ctx, const float* w, uint32_t out_dim, ui
 }
 
 int prism_hip_palettize_dev(prism_hip_ctx* ctx, const void* d_w, uint32_t out_dim, uint32_t in_dim, uint32_t k,
-                            uint32_t max_iter, void* d_payload, void* stream) {
+                            uint32_t max_iter, const float* seeds, uint32_t nseeds, void* d_payload, void* stream) {
   if (!ctx) return PRISM_HIP_ERR_NULL;
-  int rc = check_palettize(ctx, k);
+  prism::PaletteSeeds ps;
+  int rc = check_palettize(ctx, k, seeds, nseeds, &ps);
   if (rc) return rc;
   if (out_dim == 0) return PRISM_HIP_OK;
   if (!d_payload || (!d_w && in_dim)) return fail(ctx, PRISM_HIP_ERR_NULL, "weights or payload is NULL");
   DeviceGuard g(ctx->device);
-  rc = launch_palettize(ctx, reinterpret_cast<const float*>(d_w), out_dim, in_dim, k, max_iter,
+  rc = launch_palettize(ctx, reinterpret_cast<const float*>(d_w), out_dim, in_dim, k, max_iter, ps,
                         reinterpret_cast<uint8_t*>(d_payload), pick_stream(ctx, stream));
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;

@@ -17,7 +17,8 @@ import numpy as np
 
 # Seeds of the BASELINE configurations (numpy PCG64); recorded in every
 # bench and test record.
-SEEDS = {"cfg1": 1001, "cfg2": 1002, "cfg3": 1003, "cfg4": 1004, "cfg5": 1005, "hero": 1000}
+SEEDS = {"cfg1": 1001, "cfg2": 1002, "cfg3": 1003, "cfg4": 1004, "cfg5": 1005, "hero": 1000,
+         "palettize": 1006}
 
 
 def lut_entries(bits: int) -> int:

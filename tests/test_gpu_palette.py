@@ -114,11 +114,38 @@ def test_palettize_embedding_round_trip(gpu_ctx, pe):
     assert np.array_equal(gpu_ctx.gemv(a, x), gpu_ctx.gemv(b, x))
 
 
+SEEDED = [
+    # kind, rows, cols, k, seeds
+    ("normal", 64, 896, 16, [0.01, -0.02, 0.005]),
+    ("unit", 32, 500, 16, np.linspace(-2, 2, 16).tolist()),   # k seeds: Lloyd only
+    ("int", 20, 333, 8, [3.0, -7.0, 11.0, 0.0, 5.0, 5.0]),    # repeated seed
+    ("normal", 3, 20500, 16, [0.0]),                          # workspace path
+    ("normal", 10, 5, 16, [0.1, 0.2, 0.3, 0.4, 0.5, 0.6, 0.7]),  # k = n = 5 < nseeds
+]
+
+
+@pytest.mark.parametrize("kind,rows,cols,k,seeds", SEEDED)
+def test_palettize_seeded_matches_oracle(gpu_ctx, pe, kind, rows, cols, k, seeds):
+    """compute-core's palettize_matrix_phased with calibration seeds."""
+    import torch
+    w = weights(kind, rows, cols, 7200 + rows + cols)
+    print(f"palettize seeded {kind} {rows}x{cols} k={k} nseeds={len(seeds)}", flush=True)
+    want, _ = oracle.palettize_payload(w, k, 50, threads=8, seeds=seeds)
+    assert np.array_equal(gpu_ctx.palettize(w, k, 50, seeds=seeds), want)
+    d_w = torch.from_numpy(w).cuda()
+    d_p = torch.empty(want.size, dtype=torch.uint8, device="cuda")
+    gpu_ctx.palettize_dev(d_w, rows, cols, d_p, k, 50, seeds=seeds)
+    torch.cuda.synchronize()
+    assert np.array_equal(d_p.cpu().numpy(), want)
+
+
 def test_palettize_errors(gpu_ctx, pe):
     w = weights("normal", 4, 32, 7105)
     for k in (0, 17):
         with pytest.raises(pe.PrismHipError):
             gpu_ctx.palettize(w, k)
+    with pytest.raises(pe.PrismHipError):
+        gpu_ctx.palettize(w, 16, 50, seeds=[])  # the reference panics on an empty seed list
     empty = gpu_ctx.palettize(np.zeros((0, 32), np.float32))
     assert empty.size == 0
     # in_dim 0: all-zero LUTs, no index bytes (fit_palette returns no entries)

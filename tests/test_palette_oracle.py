@@ -104,13 +104,14 @@ def _frac(seed):
     return x - math.trunc(x)
 
 
-def _init_exact(ch, k):
-    """k-means++ picks on an integer channel, in exact integer arithmetic."""
+def _init_exact(ch, k, seeds=None):
+    """k-means++ picks on an integer channel, in exact integer arithmetic
+    (seeds: compute-core's calibration seeds, the first centroids)."""
     n = len(ch)
     k = min(k, n)
-    c = [ch[n // 2]]
+    c = [ch[n // 2]] if seeds is None else list(seeds[:k])
     md = [None] * n
-    for nc in range(1, k):
+    for nc in range(len(c), k):
         last = c[-1]
         for i, v in enumerate(ch):
             d = (v - last) ** 2
@@ -249,3 +250,51 @@ def test_threaded_payload_is_identical():
     a, ea = oracle.palettize_payload(w, 16, 50, threads=1)
     b, eb = oracle.palettize_payload(w, 16, 50, threads=4)
     assert np.array_equal(a, b) and np.array_equal(ea, eb)
+
+
+# ---- seeded variant (compute-core/src/quantization/palette.rs:94-201) --------
+
+def test_k_seeds_are_the_initial_palette():
+    """With k seeds there is no k-means++ step: max_iter 0 returns the seeds
+    sorted by magnitude."""
+    seeds = [0.5, -2.0, 1.25, -0.125]
+    got = oracle.fit_palette(np.linspace(-3, 3, 50, dtype=np.float32), 4, 0, seeds=seeds)
+    assert got.tolist() == _by_magnitude(seeds)
+    # entries past k are never used
+    assert oracle.fit_palette(np.linspace(-3, 3, 50, dtype=np.float32), 4, 0,
+                              seeds=seeds + [9.0, 9.5]).tolist() == _by_magnitude(seeds)
+
+
+@pytest.mark.parametrize("seed,n,k,ns", [(61, 200, 16, 3), (62, 1000, 16, 1), (63, 64, 8, 7), (64, 500, 16, 15)])
+def test_seeded_init_matches_exact_integer_picks(seed, n, k, ns):
+    rng = np.random.default_rng(seed)
+    ch = rng.integers(-40, 41, n).tolist()
+    seeds = rng.integers(-40, 41, ns).tolist()
+    want = _by_magnitude([float(v) for v in _init_exact(ch, k, seeds)])
+    got = oracle.fit_palette(np.array(ch, np.float32), k, 0, seeds=np.array(seeds, np.float32)).tolist()
+    assert got == want
+
+
+@pytest.mark.parametrize("seed,n,k,ns", [(71, 300, 16, 4), (72, 90, 6, 6)])
+def test_seeded_lloyd_step_matches_exact(seed, n, k, ns):
+    rng = np.random.default_rng(seed)
+    ch = rng.integers(-40, 41, n).tolist()
+    seeds = rng.integers(-40, 41, ns).tolist()
+    want = _by_magnitude(_lloyd1_exact(ch, _init_exact(ch, k, seeds)))
+    got = oracle.fit_palette(np.array(ch, np.float32), k, 1, seeds=np.array(seeds, np.float32)).tolist()
+    assert got == want
+
+
+def test_seeds_covering_every_value_give_an_exact_payload():
+    rng = np.random.default_rng(81)
+    vals = np.array([-0.5, -0.125, 0.0, 0.25, 1.0], np.float32)
+    w = vals[rng.integers(0, 5, (6, 300))]
+    payload, mse = oracle.palettize_payload(w, 16, 50, seeds=vals)
+    assert np.array_equal(decode(payload, 6, 300), w) and np.all(mse == 0)
+
+
+def test_empty_seed_list_is_rejected():
+    with pytest.raises(ValueError):
+        oracle.fit_palette([1.0, 2.0], 2, 5, seeds=[])
+    with pytest.raises(ValueError):
+        oracle.palettize_payload(np.ones((2, 4), np.float32), 2, 5, seeds=[])
