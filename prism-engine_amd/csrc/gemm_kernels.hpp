@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "lut_perm.hpp"
 
 namespace prism {
@@ -182,52 +184,96 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ lut, c
     }
 }
 
-// ---------------------------------------------------------------------------
-// k_gemm_w4: 4-bit prefill GEMM that decodes W straight into MFMA B-operand
-// registers (no decoded-W tile in LDS).
-//
-// * Block tile 256 (M) x 256 (N), 4 waves (one per SIMD); wave w owns all
-//   256 M rows and N columns [64w, +64): 8 x 2 tiles of
-//   v_mfma_f32_32x32x16_f16, 256 fp32 accumulators per lane (AGPRs).  Each
-//   decoded B operand feeds 8 MFMAs and each A fragment 2, which keeps the
-//   VALU decode at ~40 % and the LDS fragment reads at ~50 % of the MFMA
-//   time; the step loop is software-pipelined (next step's B decoded while
-//   the current step's MFMAs run) and interleaved with
-//   sched_group_barrier so one wave per SIMD keeps the matrix core fed.
-// * B operand (weights): lane (j = lane%32, h = lane/32) of N-subtile t
-//   always holds weight row n0 + 64w + 32t + j, so it keeps that row's LUT
-//   in 8 VGPRs as byte planes (lo / hi bytes of entries 0-3, 4-7, 8-11,
-//   12-15) for the whole K loop.  One index dword (8 nibbles) is decoded
-//   with v_perm_b32 byte selects (two 8-byte windows and a bit-3 v_bfi
-//   merge for lo and hi bytes, then two interleaving perms): 25 VALU ops
-//   for the 4 VGPRs of one MFMA B operand, which co-issue under the 8
-//   MFMAs (8 M-subtiles) that consume it.
-// * The decoded halves come out in k order (0,2,4,6,1,3,5,7) of the
-//   dword's 8 nibbles; the X tile is stored in LDS with every group of 8
-//   halves permuted the same way, so A (X) and B agree on k.
-// * X tile (A operand) 256 x 64 fp16 in LDS, double-buffered, 144-byte row
-//   pitch (16-byte fragment reads of 8 consecutive rows hit 32 distinct
-//   banks); the next K step's X tile and index chunks are loaded from global
-//   memory while the current step's MFMAs run; one barrier per K step.
-// * Per 64-wide K step a lane loads 16 index bytes of each of its two rows
-//   (bytes [32*it + 16h, +16), i.e. nibbles [64*it + 32h, +32)); MFMA step
-//   q in {0..3} uses dword q, so lane half h covers k = 64*it + 32h + 8q +
-//   {0,2,4,6,1,3,5,7}.
-// Requires K % 64 == 0.
 constexpr int GW4_BM = 256;
 constexpr int GW4_BN = 256;
 constexpr int GW4_BK = 64;
 constexpr int GW4_PITCH = GW4_BK + 8;  // halves per LDS row (144 B)
+// Buffer descriptor word 3 (gfx9-family raw buffer, 32-bit data format).
+constexpr int kGwdWord3 = 0x00020000;
+
+// ---------------------------------------------------------------------------
+// k_gemm_w4: 4-bit prefill GEMM.  W is decoded straight into MFMA B-operand
+// registers; X and the index chunks reach LDS by DMA.
+//
+// * Block tile 256 (M) x 256 (N), 4 waves (one per SIMD); wave w owns all
+//   256 M rows and N columns [64w, +64): 8 x 2 tiles of
+//   v_mfma_f32_32x32x16_f16, 256 fp32 accumulators per lane (AGPRs).  Each
+//   decoded B operand feeds 8 MFMAs and each A fragment 2.
+// * B operand (weights): lane (j = lane%32, h = lane/32) of N-subtile s
+//   always holds weight row n0 + 64w + 32s + j, so it keeps that row's LUT
+//   in 8 VGPRs as byte planes for the whole K loop, and one index dword (8
+//   nibbles) becomes one B operand with v_perm_b32 byte selects
+//   (decode_nib8_nat, 29 VALU ops) that co-issue under the MFMAs.  Per
+//   64-wide K step the lane uses 16 index bytes of each of its rows (bytes
+//   [32 it + 16h, +16)); MFMA step q uses dword q, so lane half h covers
+//   k = 64 it + 32h + 8q + 0..7, and the A fragment of the same lane holds
+//   the same k (logical chunk 4h + q of the X tile row).
+// * Both global streams -- the X tile and the index chunks -- are fetched
+//   by the LDS DMA (buffer_load ... lds) into a GWD_STAGES-deep ring of LDS
+//   stages, so no VGPR-destination global load is left in the K loop:
+//   - X part of a stage: 256 rows x 64 halves = 2048 16-byte slots,
+//     unpadded; slot (r, p) holds logical chunk p ^ f(r) of row r, f(r) =
+//     (r & 7) ^ ((r >> 3) & 1).  A 16-byte-per-lane LDS read serves 16
+//     lanes per clock on gfx950 (64 banks); the 16 rows a fragment read
+//     touches at one logical chunk then land in 16 distinct 16-byte bank
+//     groups (measured: as fast as a contiguous read, where f(r) = r & 7
+//     loses ~30 %).  One DMA instruction fills 8 rows (64 slots, lane l ->
+//     slot l): lane l loads row 8i + l/8, chunk (l%8) ^ (l/8) ^ (i & 1), a
+//     per-lane byte offset (two, by the parity of i) fixed for the whole
+//     loop, the row block and K step going into the scalar offset;
+//   - index part: 256 weight rows x 32 bytes (this K step's 64 nibbles),
+//     2 slots per row; wave w fills its own 64 rows with 2 instructions.
+// * Schedule of K step it (stage it % 3): MFMA steps 0..2 each read the next
+//   step's A fragments and decode its B operands (double buffers) under
+//   their own 16 MFMAs.  Before MFMA step 3 the wave waits for its reads of
+//   the stage (lgkmcnt) and for its own DMA of step it+1 (loads return in
+//   issue order, so vmcnt <= the 10 instructions of step it+2); the barrier
+//   then publishes step it+1's stage and frees stage it % 3, which the
+//   wave refills with step it+3.  Step it+1's index chunks and first A
+//   fragments are read under step 3's MFMAs and its first B operands are
+//   decoded after them, while the matrix core drains the queued MFMAs.
+// * Blocks are mapped XCD-aware: hardware dispatches block b to XCD b % 8;
+//   the remap gives each XCD a contiguous range of tiles (N-fastest) so the
+//   W tiles and X rows one XCD works on stay in its own L2.
+// Requires K % 64 == 0, 16-byte aligned X, an index block below 2 GiB and
+// 256 * K * 2 bytes of X per block below 2 GiB (the buffer descriptors'
+// 32-bit ranges; rows past M or N read as 0 through the range check).
+constexpr int GWD_STAGES = 3;
+constexpr int GWD_XSLOTS = GW4_BM * GW4_BK / 8;  // 16-byte X slots per stage
+constexpr int GWD_WSLOTS = GW4_BN * 2;           // 16-byte index slots per stage
+constexpr int GWD_SLOTS = GWD_XSLOTS + GWD_WSLOTS;
+
+__device__ __forceinline__ void gwd_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// One 16-byte-per-lane LDS DMA: lane l's 16 bytes at voff + soff of the
+// buffer land at LDS byte address `lds` + 16 l (lds wave-uniform).  Issued as
+// inline asm so the compiler's wait-count pass, which cannot tell the stages
+// of the ring apart, does not drain the whole ring before every LDS read;
+// the kernel's own vmcnt waits and barriers order the ring.  The kernel
+// uses M0 for nothing else.
+__device__ __forceinline__ void gwd_dma16(__amdgpu_buffer_rsrc_t r, const void* lds, uint32_t voff, uint32_t soff) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(la), "v"(voff), "s"(r), "s"(soff)
+               : "memory", "m0");
+}
+
+template <int N_>
+__device__ __forceinline__ void gwd_wait_vm() {
+  // vmcnt <= N_, expcnt and lgkmcnt unconstrained (gfx9 s_waitcnt encoding)
+  static_assert(N_ >= 0 && N_ < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N_ & 0xF) | ((N_ >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                  const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
                                                  uint32_t N, uint32_t K) {
-  constexpr int BM = GW4_BM, BN = GW4_BN, BK = GW4_BK, P = GW4_PITCH;
-  __shared__ __attribute__((aligned(16))) uint16_t sX[2][BM * P];
+  constexpr int BM = GW4_BM, BN = GW4_BN, BK = GW4_BK, S = GWD_STAGES, SL = GWD_SLOTS, XS = GWD_XSLOTS;
+  constexpr int OPS = 10;  // DMA instructions per wave per K step (8 X + 2 index)
+  __shared__ __attribute__((aligned(16))) uint4 sx[S * SL];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;  // wave tile: all 256 M rows, N cols [64*wave, +64)
+  const int wave = tid >> 6;
   const int j = lane & 31, h = lane >> 5;
 
   const uint32_t mt = (M + BM - 1) / BM;
@@ -235,64 +281,43 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   const uint32_t ntiles = mt * nt;
   uint32_t t = blockIdx.x;
   {
-    // XCD-aware: block b runs on XCD b % 8; XCD x takes a contiguous tile
-    // range, N-fastest, so its W rows and X rows stay in its own L2.
     const uint32_t per = ntiles / 8, rem = ntiles % 8;
     const uint32_t xcd = t % 8, slot = t / 8;
-    const uint32_t start = xcd * per + (xcd < rem ? xcd : rem);
-    t = start + slot;
+    t = xcd * per + (xcd < rem ? xcd : rem) + slot;
   }
   const uint32_t n0 = (t % nt) * BN;
   const uint32_t m0 = (t / nt) * BM;
   const uint32_t row_bytes = K / 2;
   const uint32_t nk = K / BK;
 
-  // ---- this lane's two weight rows: LUT planes and index row pointers
+  // ---- LUT planes of this lane's two weight rows (rows past N: the last row)
   LutPlanes pl[2];
-  const uint8_t* wrow[2];
 #pragma unroll
   for (int s = 0; s < 2; s++) {
     uint32_t n = n0 + 64 * wave + 32 * s + j;
     n = n < N ? n : N - 1;
     const uint4* lr = reinterpret_cast<const uint4*>(lut + (size_t)n * 32);
     pl[s] = make_planes(lr[0], lr[1]);
-    wrow[s] = idx + (size_t)n * row_bytes + 16 * h;
   }
+  // ---- DMA sources; reads past the descriptors' ranges return 0
+  const uint32_t live = (M - m0 < (uint32_t)BM) ? M - m0 : (uint32_t)BM;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(X + (size_t)m0 * K), (short)0, (int)(live * K * 2u), kGwdWord3);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)idx, (short)0, (int)(N * row_bytes), kGwdWord3);
+  const uint32_t lr8 = (uint32_t)lane >> 3, lc = ((uint32_t)lane & 7u) ^ lr8;
+  const uint32_t xv0 = (64u * wave + lr8) * K * 2u + 16u * lc;  // even DMA index
+  const uint32_t xv1 = xv0 ^ 16u;                                // odd: chunk lc ^ 1
+  const uint32_t wv = (n0 + 64u * wave + ((uint32_t)lane >> 1)) * row_bytes + 16u * ((uint32_t)lane & 1u);
 
-  // ---- X tile loads: 256 rows x 128 B = 2048 chunks of 16 B, 8 per thread
-  uint4 xs[8];
-  auto load_x = [&](uint32_t it) {
+  auto issue = [&](uint32_t it, int stage) {
+    uint4* st = sx + stage * SL;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int c = tid + 256 * i;
-      uint32_t m = m0 + (c >> 3);
-      m = m < M ? m : M - 1;
-      xs[i] = *reinterpret_cast<const uint4*>(X + (size_t)m * K + (size_t)it * BK + 8 * (c & 7));
-    }
-  };
-  // permute each group of 8 halves to k order (0,2,4,6,1,3,5,7) and store
-  auto store_x = [&](int buf) {
+    for (int i = 0; i < 8; i++)
+      gwd_dma16(rx, st + 64 * (8 * wave + i), (i & 1) ? xv1 : xv0, (uint32_t)i * 16u * K + it * 128u);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int c = tid + 256 * i;
-      const uint4 v = xs[i];
-      uint4 o;
-      o.x = __builtin_amdgcn_perm(v.y, v.x, 0x05040100u);
-      o.y = __builtin_amdgcn_perm(v.w, v.z, 0x05040100u);
-      o.z = __builtin_amdgcn_perm(v.y, v.x, 0x07060302u);
-      o.w = __builtin_amdgcn_perm(v.w, v.z, 0x07060302u);
-      *reinterpret_cast<uint4*>(&sX[buf][(c >> 3) * P + 8 * (c & 7)]) = o;
-    }
-  };
-  uint4 wc[2], wn2[2];
-  auto load_w = [&](uint32_t it, uint4 (&dst)[2]) {
-#pragma unroll
-    for (int s = 0; s < 2; s++) {
-      dst[s] = *reinterpret_cast<const uint4*>(wrow[s] + (size_t)it * 32);
-      // opaque to the optimizer: keep the loaded words in registers instead
-      // of re-issuing the (read-only) load next to a later use
-      asm volatile("" : "+v"(dst[s].x), "+v"(dst[s].y), "+v"(dst[s].z), "+v"(dst[s].w));
-    }
+    for (int i = 0; i < 2; i++)
+      gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv, (uint32_t)i * 32u * row_bytes + it * 32u);
   };
   auto wdword = [](const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; };
 
@@ -304,57 +329,103 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][s][e] = 0.0f;
 
-  load_x(0);
-  load_w(0, wc);
-  store_x(0);
-  __syncthreads();
-  // Software pipeline over MFMA steps: the B operands of the next step are
-  // decoded while the current step's 16 MFMAs run (two register sets,
-  // indexed by step parity); A fragments are read next to their MFMAs.
+  // A fragment of M-subtile i, logical chunk c (= 4h + q): row r = 32i + j,
+  // slot (r, c ^ f(r)) with f(r) == f(j).  Index chunk of row s: slot
+  // 2 * (64 wave + 32 s + j) + h of the index part.
+  const uint32_t arow = (uint32_t)j * 8u;
+  const uint32_t asw = ((uint32_t)j & 7u) ^ (((uint32_t)j >> 3) & 1u);
+  const uint32_t wsl = 2u * (64u * wave + j) + h;
+
+  half8_t a[2][8];
   half8_t bop[2][2];
-  bop[0][0] = decode_nib8(wc[0].x, pl[0]);
-  bop[0][1] = decode_nib8(wc[1].x, pl[1]);
-  int buf = 0;
-  for (uint32_t it = 0; it < nk; it++) {
-    // next K block's global loads (clamped on the last block: a re-read of
-    // the same tile, L2 hits) -- keeps the loop body one straight-line block
-    const uint32_t itn = it + 1 < nk ? it + 1 : it;
-    load_x(itn);
-    load_w(itn, wn2);
-    const uint16_t* xb = &sX[buf][j * P + 32 * h];
+  uint4 wch[2];
+  auto read_first = [&](const uint4* st) {  // index chunks + MFMA step 0's A fragments
+    wch[0] = st[XS + wsl];
+    wch[1] = st[XS + wsl + 64];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
+    for (int i = 0; i < 8; i++) a[0][i] = __builtin_bit_cast(half8_t, st[256 * i + arow + ((4u * h) ^ asw)]);
+  };
+  auto decode_b = [&](int buf, int q) {
+    bop[buf][0] = decode_nib8_nat(wdword(wch[0], q), pl[0]);
+    bop[buf][1] = decode_nib8_nat(wdword(wch[1], q), pl[1]);
+  };
+
+  // Prologue: steps 0..2 in flight, step 0 landed everywhere.
+  issue(0, 0);
+  if (nk > 1) issue(1, 1);
+  if (nk > 2) issue(2, 2);
+  if (nk > 2)
+    gwd_wait_vm<2 * OPS>();
+  else if (nk > 1)
+    gwd_wait_vm<OPS>();
+  else
+    gwd_wait_vm<0>();
+  gwd_barrier();
+  read_first(sx);
+  decode_b(0, 0);
+
+  auto kstep = [&](auto sc_tag, uint32_t it) {
+    constexpr int SC = decltype(sc_tag)::value;
+    constexpr int SNX = (SC + 1) % 3;
+    const uint4* st = sx + SC * SL;
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
       const int cur = q & 1, nxt = cur ^ 1;
-      half8_t a[8];
 #pragma unroll
-      for (int i = 0; i < 8; i++) a[i] = *reinterpret_cast<const half8_t*>(xb + 32 * i * P + 8 * q);
-      if (q < 3) {
-        bop[nxt][0] = decode_nib8(wdword(wc[0], q + 1), pl[0]);
-        bop[nxt][1] = decode_nib8(wdword(wc[1], q + 1), pl[1]);
-      } else {
-        bop[nxt][0] = decode_nib8(wn2[0].x, pl[0]);
-        bop[nxt][1] = decode_nib8(wn2[1].x, pl[1]);
-      }
+      for (int i = 0; i < 8; i++)
+        a[nxt][i] = __builtin_bit_cast(half8_t, st[256 * i + arow + ((4u * h + q + 1) ^ asw)]);
+      decode_b(nxt, q + 1);
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bop[cur][0], acc[i][0], 0, 0, 0);
-        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bop[cur][1], acc[i][1], 0, 0, 0);
+        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], bop[cur][0], acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], bop[cur][1], acc[i][1], 0, 0, 0);
       }
-      // interleave: per MFMA pair, one A fragment read and ~3 VALU ops each
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
       }
     }
-    store_x(buf ^ 1);
-    wc[0] = wn2[0];
-    wc[1] = wn2[1];
-    __syncthreads();
-    buf ^= 1;
+    // MFMA step 3 (operands in buffer 1).  Its B decode, issued under step
+    // 2's MFMAs, is pinned ahead of the barrier (the compiler would sink it
+    // past the asm).
+    asm volatile("" : "+v"(bop[1][0]), "+v"(bop[1][1]));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage SC are done
+    if (it + 2 < nk)
+      gwd_wait_vm<OPS>();
+    else
+      gwd_wait_vm<0>();
+    gwd_barrier();
+    if (it + 3 < nk) issue(it + 3, SC);
+    const bool more = it + 1 < nk;
+    const uint4* sn = sx + SNX * SL;
+    if (more) {
+      wch[0] = sn[XS + wsl];
+      wch[1] = sn[XS + wsl + 64];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      if (more) a[0][i] = __builtin_bit_cast(half8_t, sn[256 * i + arow + ((4u * h) ^ asw)]);
+      acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1][i], bop[1][0], acc[i][0], 0, 0, 0);
+      acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1][i], bop[1][1], acc[i][1], 0, 0, 0);
+    }
+    if (more) decode_b(0, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read: index chunks
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    }
+    __builtin_amdgcn_sched_group_barrier(0x002, 64, 0);  // VALU: next step's decode
+  };
+
+  for (uint32_t it = 0; it < nk; it += 3) {
+    kstep(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < nk) kstep(std::integral_constant<int, 1>{}, it + 1);
+    if (it + 2 < nk) kstep(std::integral_constant<int, 2>{}, it + 2);
   }
 
   // ---- epilogue: D lane layout: col j = lane%32, row 8*(e/4) + 4*(lane/32) + e%4

@@ -10,10 +10,8 @@
 //     more v_perm) merges the two windows with v_bfi;
 //   * that is done for the lo and the hi bytes of the even and the odd
 //     nibbles, and two interleaving perms per parity rebuild the fp16
-//     values: 25 VALU ops per dword.
-// The values come out in k order (0,2,4,6,1,3,5,7), i.e. the fp16 pairs
-// (e0,e2) (e4,e6) (e1,e3) (e5,e7); the consumer permutes the other operand
-// the same way (x_pairs_for_perm below for a GEMV, the X tile for the GEMM).
+//     values: 25 VALU ops per dword give the pairs (e0,e2) (e4,e6) (e1,e3)
+//     (e5,e7); four more perms put them in k order (29 ops).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -58,26 +56,18 @@ __device__ __forceinline__ void decode_nib8_pairs(uint32_t w, const LutPlanes& P
   o[3] = __builtin_amdgcn_perm(ho, lo, 0x07030602u);
 }
 
-// The same, as one MFMA operand (8 halves).
-__device__ __forceinline__ half8_t decode_nib8(uint32_t w, const LutPlanes& P) {
-  uint32_t o[4];
-  decode_nib8_pairs(w, P, o);
+// 8 nibbles -> one MFMA operand of 8 halves in k order, (e0,e1) (e2,e3)
+// (e4,e5) (e6,e7).
+__device__ __forceinline__ half8_t decode_nib8_nat(uint32_t w, const LutPlanes& P) {
+  uint32_t t[4];
+  decode_nib8_pairs(w, P, t);
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
   u32x4v v;
-  v.x = o[0];
-  v.y = o[1];
-  v.z = o[2];
-  v.w = o[3];
+  v.x = __builtin_amdgcn_perm(t[2], t[0], 0x05040100u);
+  v.y = __builtin_amdgcn_perm(t[2], t[0], 0x07060302u);
+  v.z = __builtin_amdgcn_perm(t[3], t[1], 0x05040100u);
+  v.w = __builtin_amdgcn_perm(t[3], t[1], 0x07060302u);
   return __builtin_bit_cast(half8_t, v);
-}
-
-// x dwords (x0,x1) (x2,x3) (x4,x5) (x6,x7) -> (x0,x2) (x4,x6) (x1,x3) (x5,x7),
-// the pairing decode_nib8_pairs produces.
-__device__ __forceinline__ void x_pairs_for_perm(const uint32_t* xd, uint32_t (&o)[4]) {
-  o[0] = __builtin_amdgcn_perm(xd[1], xd[0], 0x05040100u);
-  o[1] = __builtin_amdgcn_perm(xd[3], xd[2], 0x05040100u);
-  o[2] = __builtin_amdgcn_perm(xd[1], xd[0], 0x07060302u);
-  o[3] = __builtin_amdgcn_perm(xd[3], xd[2], 0x07060302u);
 }
 
 }  // namespace prism

@@ -263,8 +263,11 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
   if (!fast) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
-  if (bits == 4 && K % prism::GW4_BK == 0) {
-    // register-decode MFMA kernel (gemm_kernels.hpp, k_gemm_w4)
+  // 4-bit, K % 64 == 0: the MFMA kernel with register decode and LDS-DMA
+  // staging (gemm_kernels.hpp, k_gemm_w4); its buffer descriptors address
+  // the index block and one block's X rows with 32-bit ranges.
+  if (bits == 4 && K % prism::GW4_BK == 0 && (uint64_t)N * (K / 2) < (1ull << 31) &&
+      (uint64_t)prism::GW4_BM * K * 2 < (1ull << 31)) {
     const uint32_t tiles4 =
         ((M + prism::GW4_BM - 1) / prism::GW4_BM) * ((N + prism::GW4_BN - 1) / prism::GW4_BN);
     const uint8_t* lut = w->lut();
