@@ -121,11 +121,8 @@ struct AttnArgs {
 //    uses its own dequantized copy, so no workgroup waits for another;
 //  * attention_cpu (evaluator.rs:104-146) over sl = kv_len + 1 positions:
 //    split s of a head takes positions [s*C, (s+1)*C), C = ceil(sl / S).
-//    Scores: one position per thread, a sequential fp32 dot of fp16 q and
-//    dequantized fp16 k in the reference's order, divided by sqrt(64).
-//    Values: lane l owns dims 4*(l%16)..+3 of positions l/16 + 4j (4w +
-//    l/16 + 4*W*j for W waves), so every V load is a contiguous 256-byte
-//    wave access.
+//    Scores: fp32 dots of fp16 q and dequantized fp16 k (four sequential
+//    16-dim folds added pairwise), divided by sqrt(64).
 //    A split writes (m, sum_p e^(s_p - m), sum_p e^(s_p - m) v_p) to `part`;
 //    the O-projection GEMV's prologue (kEpiAttnIn, attn_combine) rescales
 //    the S partials to the head's max, adds them and scales once by
@@ -133,24 +130,46 @@ struct AttnArgs {
 //    visible (device-scope fences inside this kernel would write back and
 //    invalidate each XCD's whole L2).  Max is exact; the exp, the
 //    sums and the output are fp32 in another order than the reference's folds.
-// Every global K/V load of a split is issued before the new token's
-// quantization and RoPE.  sl <= kAttnSplits * kAttnThreads * kAttnPasses.
+// Latency layout: the loads that gate the setup (q, its RoPE row, the new
+// token's K and V, all L2-resident) are issued before the split's K rows and
+// V words (HBM), since loads return in issue order.  The new token's max
+// |k|, |v| are reductions inside wave 0 (kv_dim <= 256: 4 values per lane).
+// One barrier publishes q and the new token's dequantized K/V.  Then each of
+// the 16 waves runs an online softmax over its own 16-position slice of
+// every pass with wave shuffles only: a score is 4 lanes' sequential folds
+// over 16 dims each, added pairwise; lane l owns value dims 4*(l%16)..+3 of
+// positions l/16 + 4j, j < 4.  One last barrier combines the waves' (m, sum,
+// out) partials into the split's.
+// sl <= kAttnSplits * kAttnPassPos * kAttnPasses.
 constexpr int kAttnSplits = 4;
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 1024;
+constexpr int kAttnPassPos = 256;  // positions per pass: 16 per wave
 constexpr int kAttnPasses = 8;
-constexpr int kAttnMaxSeq = kAttnSplits * kAttnThreads * kAttnPasses;
+constexpr int kAttnMaxSeq = kAttnSplits * kAttnPassPos * kAttnPasses;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
 #pragma clang fp contract(off)
   constexpr int HD = 64;
   constexpr int T = kAttnThreads;
   constexpr int NW = T / 64;
   constexpr int S = kAttnSplits;
-  constexpr int VJ = T / (4 * NW);  // V words per lane per pass: positions 4w + l/16 + 4*NW*j
+  constexpr int PW = kAttnPassPos / NW;  // positions per wave per pass (16)
+  constexpr int VJ = PW / 4;             // V words per lane per slice
+  static_assert(PW == 16, "lane roles assume 16 positions per wave");
   __shared__ float s_q[HD];
   __shared__ float s_knew[HD], s_vnew[HD];
-  __shared__ float s_red[2 * NW];
-  __shared__ float s_e[T];
-  __shared__ float s_out[NW][HD];
+  __shared__ float s_part[NW][2 + HD];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t h = blockIdx.x / S, sp = blockIdx.x % S;
@@ -167,22 +186,42 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
   const uint16_t* qh = a.qkv + (size_t)h * HD;
   const uint16_t* knew = a.qkv + (size_t)a.nh * HD;
   const uint16_t* vnew = knew + kvd;
-  const uint32_t dg = lane & 15, psub = lane >> 4;
+  const uint32_t ps = lane >> 2, qd = lane & 3;     // score roles: position, 16-dim quarter
+  const uint32_t dg = lane & 15, psub = lane >> 4;  // value roles
 
-  uint4 kr[HD / 16];
+  // ---- setup loads: q and its RoPE row; the new token's K and V
+  float qx0 = 0.0f, qx1 = 0.0f;
+  float2 cs = make_float2(0.0f, 0.0f);
+  if (tid < HD / 2) {
+    cs = a.rope[(size_t)pos * (HD / 2) + tid];
+    qx0 = h2f(qh[tid]);
+    qx1 = h2f(qh[tid + HD / 2]);
+  }
+  float kn[4], vn[4];
+  if (has_new && wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t e = lane + 64 * i;
+      kn[i] = e < kvd ? h2f(knew[e]) : 0.0f;
+      vn[i] = e < kvd ? h2f(vnew[e]) : 0.0f;
+    }
+  }
+  asm volatile("" ::: "memory");  // the K/V loads below issue after these
+
+  // ---- one pass = kAttnPassPos positions; wave w the slice [base + 16w, +16)
+  uint4 kr;
   float krs;
   uint32_t vw[VJ];
   float vrs[VJ];
   auto load_pass = [&](uint32_t base) {
-    const uint32_t p = base + tid;
+    const uint32_t q0 = base + PW * wave;
+    const uint32_t p = q0 + ps;
     const uint32_t pc = p < len0 ? p : last;
-    const uint4* kp = reinterpret_cast<const uint4*>(a.kq + (size_t)pc * kvd + kvh * HD);
-#pragma unroll
-    for (int i = 0; i < HD / 16; i++) kr[i] = kp[i];
+    kr = reinterpret_cast<const uint4*>(a.kq + (size_t)pc * kvd + kvh * HD)[qd];
     krs = a.ks[pc];
 #pragma unroll
     for (int j = 0; j < VJ; j++) {
-      const uint32_t pv = base + 4 * wave + psub + 4 * NW * j;
+      const uint32_t pv = q0 + psub + 4 * j;
       const uint32_t pvc = pv < len0 ? pv : last;
       vw[j] = *reinterpret_cast<const uint32_t*>(a.vq + (size_t)pvc * kvd + kvh * HD + 4 * dg);
       vrs[j] = a.vs[pvc];
@@ -190,85 +229,82 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
   };
   if (p0 < p1) load_pass(p0);
 
-  // ---- new token's K and V (only the splits holding position kv_len):
-  // kv_dim values per matrix, strided over the workgroup's threads
-  if (has_new) {
+  if (has_new && wave == 0) {
     float kmax = 0.0f, vmax = 0.0f;
-    for (uint32_t i = tid; i < kvd; i += T) {
-      kmax = fmaxf(kmax, fabsf(h2f(knew[i])));
-      vmax = fmaxf(vmax, fabsf(h2f(vnew[i])));
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      kmax = fmaxf(kmax, fabsf(kn[i]));
+      vmax = fmaxf(vmax, fabsf(vn[i]));
     }
-    const float ksc = kv_scale(block_max(kmax, s_red));
-    const float vsc = kv_scale(block_max(vmax, s_red + NW));
+    const float ksc = kv_scale(wave_max(kmax));
+    const float vsc = kv_scale(wave_max(vmax));
     if (h == 0) {
-      for (uint32_t i = tid; i < kvd; i += T) {
-        a.kq[(size_t)len0 * kvd + i] = kv_q(h2f(knew[i]), ksc);
-        a.vq[(size_t)len0 * kvd + i] = kv_q(h2f(vnew[i]), vsc);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t e = lane + 64 * i;
+        if (e < kvd) {
+          a.kq[(size_t)len0 * kvd + e] = kv_q(kn[i], ksc);
+          a.vq[(size_t)len0 * kvd + e] = kv_q(vn[i], vsc);
+        }
       }
-      if (tid == 0) {
+      if (lane == 0) {
         a.ks[len0] = ksc;
         a.vs[len0] = vsc;
       }
     }
-    for (uint32_t i = tid; i < (uint32_t)HD; i += T) {
-      s_knew[i] = kv_dq(kv_q(h2f(knew[kvh * HD + i]), ksc), 1.0f / ksc);
-      s_vnew[i] = kv_dq(kv_q(h2f(vnew[kvh * HD + i]), vsc), 1.0f / vsc);
-    }
+    // this head's 64 dims: element kvh * 64 + lane is value kvh of the lane
+    float kh = kn[0], vh = vn[0];
+#pragma unroll
+    for (int i = 1; i < 4; i++)
+      if ((uint32_t)i == kvh) {
+        kh = kn[i];
+        vh = vn[i];
+      }
+    s_knew[lane] = kv_dq(kv_q(kh, ksc), 1.0f / ksc);
+    s_vnew[lane] = kv_dq(kv_q(vh, vsc), 1.0f / vsc);
   }
-
-  // ---- RoPE on q (pairs j, j + 32)
   if (tid < HD / 2) {
-    const float2 cs = a.rope[(size_t)pos * (HD / 2) + tid];
-    const float x0 = h2f(qh[tid]), x1 = h2f(qh[tid + HD / 2]);
-    s_q[tid] = h2f(f2h(x0 * cs.x - x1 * cs.y));
-    s_q[tid + HD / 2] = h2f(f2h(x0 * cs.y + x1 * cs.x));
+    s_q[tid] = h2f(f2h(qx0 * cs.x - qx1 * cs.y));
+    s_q[tid + HD / 2] = h2f(f2h(qx0 * cs.y + qx1 * cs.x));
   }
   __syncthreads();
 
+  // ---- this wave's online softmax over its slices
   const float den = sqrtf((float)HD);
   float m_run = -INFINITY, s_run = 0.0f;
   float o4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (uint32_t base = p0; base < p1; base += T) {
-    if (base != p0) {
-      __syncthreads();  // s_e of the previous pass is consumed
-      load_pass(base);
-    }
-    const uint32_t p = base + tid;
-    float sc = -INFINITY;
-    if (p < p1) {
-      float sdot = 0.0f;
-      if (p < len0) {
-        const float rs = 1.0f / krs;
-        const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kr[0]);
+  for (uint32_t base = p0; base < p1; base += kAttnPassPos) {
+    if (base != p0) load_pass(base);
+    const uint32_t q0 = base + PW * wave;
+    if (q0 >= p1) continue;  // uniform per wave
+    const uint32_t p = q0 + ps;
+    float part = 0.0f;
+    if (p < len0) {
+      const float rs = 1.0f / krs;
+      const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w};
 #pragma unroll
-        for (int d = 0; d < HD; d++) sdot += s_q[d] * kv_dq((int8_t)(kw[d / 4] >> (8 * (d % 4))), rs);
-      } else {
+      for (int d = 0; d < 16; d++)
+        part += s_q[16 * qd + d] * kv_dq((int8_t)(kw[d / 4] >> (8 * (d % 4))), rs);
+    } else {
 #pragma unroll
-        for (int d = 0; d < HD; d++) sdot += s_q[d] * s_knew[d];
-      }
-      sc = sdot / den;
+      for (int d = 0; d < 16; d++) part += s_q[16 * qd + d] * s_knew[16 * qd + d];
     }
-    const float m_new = fmaxf(m_run, block_max(sc, s_red));
-    const float corr = expf(m_run - m_new);  // 0 on the first pass
+    // quarters (0+1) + (2+3): the same value in all 4 lanes of a position
+    part += __shfl_xor(part, 1, 64);
+    part += __shfl_xor(part, 2, 64);
+    const float sc = (p < p1) ? part / den : -INFINITY;
+    const float m_new = fmaxf(m_run, wave_max(sc));  // finite: the slice holds a position
+    const float corr = expf(m_run - m_new);          // 0 on the first slice
     const float e = (p < p1) ? expf(sc - m_new) : 0.0f;
-    s_e[tid] = e;
-    float esum = e;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) esum += __shfl_xor(esum, off, 64);
-    __syncthreads();
-    if (lane == 0) s_red[NW + wave] = esum;
-    __syncthreads();
-    float bsum = 0.0f;
-    for (int w = 0; w < NW; w++) bsum += s_red[NW + w];
-    s_run = s_run * corr + bsum;
+    s_run = s_run * corr + wave_sum(qd == 0 ? e : 0.0f);
     m_run = m_new;
 #pragma unroll
     for (int c = 0; c < 4; c++) o4[c] *= corr;
 #pragma unroll
     for (int j = 0; j < VJ; j++) {
-      const uint32_t pv = base + 4 * wave + psub + 4 * NW * j;
+      const uint32_t pv = q0 + psub + 4 * j;
+      const float ev = __shfl(e, (int)(4 * (psub + 4 * j)), 64);
       if (pv >= p1) continue;
-      const float ev = s_e[pv - base];
       if (pv < len0) {
         const float rs = 1.0f / vrs[j];
 #pragma unroll
@@ -280,7 +316,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
     }
   }
 
-  // ---- this split's partial: (m, sum, unnormalised output)
+  // ---- waves' partials -> this split's (m, sum, unnormalised output)
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     o4[c] += __shfl_xor(o4[c], 16, 64);
@@ -288,18 +324,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
   }
   if (psub == 0) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) s_out[wave][4 * dg + c] = o4[c];
+    for (int c = 0; c < 4; c++) s_part[wave][2 + 4 * dg + c] = o4[c];
+  }
+  if (lane == 0) {
+    s_part[wave][0] = m_run;
+    s_part[wave][1] = s_run;
   }
   __syncthreads();
-  float* mypart = a.part + ((size_t)h * S + sp) * (2 + HD);
   if (tid < HD) {
-    float v = 0.0f;
-    for (int w = 0; w < NW; w++) v += s_out[w][tid];
-    mypart[2 + tid] = v;
-  }
-  if (tid == 0) {
-    mypart[0] = m_run;
-    mypart[1] = s_run;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; w++) M = fmaxf(M, s_part[w][0]);
+    float tot = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      const float mw = s_part[w][0];
+      const float f = (mw == -INFINITY) ? 0.0f : expf(mw - M);
+      tot += s_part[w][1] * f;
+      o += s_part[w][2 + tid] * f;
+    }
+    float* mypart = a.part + ((size_t)h * S + sp) * (2 + HD);
+    mypart[2 + tid] = o;
+    if (tid == 0) {
+      mypart[0] = M;
+      mypart[1] = tot;
+    }
   }
 }
 
