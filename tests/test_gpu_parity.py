@@ -124,7 +124,9 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
 
 
 @pytest.mark.parametrize("bits,M,N,K", [(4, 64, 256, 512), (4, 77, 200, 96), (8, 40, 130, 256),
-                                        (4, 3, 5, 64), (4, 10, 20, 40), (4, 300, 1000, 1024)])
+                                        (4, 3, 5, 64), (4, 10, 20, 40), (4, 300, 1000, 1024),
+                                        # 2, 3 and 5 K steps of 64: every tail of the 3-stage ring
+                                        (4, 40, 300, 128), (4, 70, 260, 192), (4, 257, 513, 320)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
