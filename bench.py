@@ -40,8 +40,9 @@ HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE x 1,
-# scales from a 64 MiB copy): profiles/k_gemv_tile_hero_4bit_b1_pmc.md
-PMC_TRAFFIC = {"hero": 30645376}
+# scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_tile_hero_4bit_b1_pmc.md,
+# profiles/k_gemv8_mfma_cfg4_8bit_b8.md
+PMC_TRAFFIC = {("hero", 1): 30645376, ("cfg4", 8): 67152856}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
@@ -460,8 +461,12 @@ def main() -> int:
                   if args.workload == "hero" else
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": PMC_TRAFFIC.get(args.workload) if batch == WORKLOADS[args.workload][4] else None}
-    kernel_name = {"gemv": "k_gemv_tile", "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": PMC_TRAFFIC.get((args.workload, batch))}
+    # the library's GEMV dispatch: 8-bit at 5..8 vectors and >= 4096 rows
+    # runs on the matrix cores
+    mfma8 = kind == "gemv" and bits == 8 and 5 <= batch <= 8 and N >= 4096 and K % 128 == 0
+    kernel_name = {"gemv": "k_gemv8_mfma" if mfma8 else "k_gemv_tile",
+                   "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
                    "gemm": "k_gemm_w4" if bits == 4 else "k_gemm"}[kind]
     roof["kernel"] = kernel_name
     roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb

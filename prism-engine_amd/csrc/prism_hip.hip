@@ -20,6 +20,7 @@
 #include "gemm_kernels.hpp"
 #include "gemv_kernels.hpp"
 #include "gemv_tile.hpp"
+#include "gemv_mfma.hpp"
 #include "palette_kernels.hpp"
 #include "step_kernels.hpp"
 
@@ -227,13 +228,39 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
   a.K = K;
   a.eps = eps;
   a.xpart = xpart;
-  for (uint32_t b0 = 0; b0 < nb; b0 += 8) {
-    const uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
+  for (uint32_t b0 = 0; b0 < nb;) {
+    uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
     a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
-    a.nb = chunk;
-    const TilePlan p = plan_tile(bits, N, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x), epi);
     void* args[] = {&a};
+    // 8-bit, 5..8 batch vectors, 4096 rows or more: the matrix-core kernel
+    // (gemv_mfma.hpp).  Against the tile kernel on MI355X: 19.6 vs 26.0 us
+    // at 14336x4096 and 8 vectors, 29.8 vs 2 x 20 at 4096x14336, 6.1 vs 7.8
+    // at 4864x896; no faster at 3..4 vectors, slower at 896 rows (28
+    // workgroups).
+    if (bits == 8 && !dual && !epi && chunk >= 5 && N >= 4096 && K % prism::kG8Group == 0 &&
+        (uint64_t)N * K < (1ull << 31) && reinterpret_cast<uintptr_t>(a.x) % 16 == 0) {
+      a.nb = chunk;
+      HIP_TRY(ctx, hipLaunchKernel(reinterpret_cast<const void*>(&prism::k_gemv8_mfma),
+                                   dim3((N + prism::kG8Rows - 1) / prism::kG8Rows), dim3(64 * prism::kG8Waves),
+                                   args, 0, st));
+      b0 += chunk;
+      continue;
+    }
+    TilePlan p = plan_tile(bits, N, K, chunk, dual, reinterpret_cast<uintptr_t>(a.x), epi);
+    // rows too long for the tile kernel's registers at this many vectors:
+    // fewer vectors per pass (each pass streams the weights again, still far
+    // cheaper than the generic kernel: 2 x 20 us against 830 us for 8
+    // vectors on 4096x14336 8-bit)
+    for (uint32_t c = chunk; !p.fn && c > 1 && !epi && !dual;) {
+      c = c > 4 ? 4 : c > 2 ? 2 : 1;
+      const TilePlan q = plan_tile(bits, N, K, c, dual, reinterpret_cast<uintptr_t>(a.x), epi);
+      if (q.fn) {
+        p = q;
+        chunk = c;
+      }
+    }
+    a.nb = chunk;
     if (p.fn) {
       const uint32_t grid = (N + (uint32_t)p.R - 1) / (uint32_t)p.R;
       HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(p.threads), args, p.lds, st));
@@ -248,6 +275,7 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
                        : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, false>);
       HIP_TRY(ctx, hipLaunchKernel(fn, dim3(N), dim3(64), args, 0, st));
     }
+    b0 += chunk;
   }
   return PRISM_HIP_OK;
 }

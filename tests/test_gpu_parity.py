@@ -71,7 +71,30 @@ def test_gemv_batch(pe, oracle, gpu_ctx, bits, N, K, batch):
     w.free()
 
 
-@pytest.mark.parametrize("bits,N,K", [(4, 4864, 896), (4, 1000, 4096), (8, 700, 4096), (4, 33, 40), (8, 20, 24)])
+@pytest.mark.parametrize("bits,N,K,batch", [
+    (8, 14336, 4096, 5), (8, 14336, 4096, 6),   # matrix-core kernel (8-bit, 5..8 vectors, N >= 4096)
+    (8, 4100, 1024, 7),                          # ragged last 32-row workgroup
+    (8, 4096, 14336, 8),                         # long rows on the matrix cores
+    (8, 4096, 14336, 13),                        # 8 + 5 vectors: two matrix-core passes
+    (4, 4096, 14336, 8),                         # rows too long for 8 vectors a pass: 4 + 4
+    (8, 2048, 14336, 6),                         # too few rows for the matrix cores: 4 + 2
+    (4, 64, 20000, 7),                           # 2 + 2 + 2 + 1
+])
+def test_gemv_batch_wide(pe, oracle, gpu_ctx, bits, N, K, batch):
+    """Batches past 4 vectors: the 8-bit matrix-core kernel and the tile
+    kernel's narrower passes for rows too long for 8 vectors at once."""
+    t = pe.synth_tensor(N, K, bits, seed=batch + bits + K)
+    x = pe.synth_x(batch, K, seed=batch + 17)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gemv {bits}-bit {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    ref = oracle.gemv(x, t.payload, N, K, bits, threads=8)
+    _check(y, ref, f"{bits}-bit {N}x{K} batch {batch}")
+    w.free()
+
+
+@pytest.mark.parametrize("bits,N,K", [(4, 4864, 896), (4, 1000, 4096), (8, 700, 4096), (4, 33, 40), (8, 20, 24),
+                                      (8, 4096, 1024)])
 def test_decode_bit_exact_through_gemv(pe, gpu_ctx, bits, N, K):
     """One-hot x (x = e_k) makes every output the decoded weight itself:
     y[r] = LUT_r[idx(r, k)] exactly, through the GEMV kernel's own decode."""
