@@ -41,8 +41,8 @@ FP16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE x 1,
 # scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_tile_hero_4bit_b1_pmc.md,
-# profiles/k_gemv8_mfma_cfg4_8bit_b8.md
-PMC_TRAFFIC = {("hero", 1): 30645376, ("cfg4", 8): 67152856}
+# profiles/k_gemv_mfma_hero_4bit_b8.md, profiles/k_gemv_mfma_cfg4_8bit_b8.md
+PMC_TRAFFIC = {("hero", 1): 30645376, ("hero", 8): 31139398, ("cfg4", 8): 67160340}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
@@ -462,10 +462,11 @@ def main() -> int:
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": PMC_TRAFFIC.get((args.workload, batch))}
-    # the library's GEMV dispatch: 8-bit at 5..8 vectors and >= 4096 rows
-    # runs on the matrix cores
-    mfma8 = kind == "gemv" and bits == 8 and 5 <= batch <= 8 and N >= 4096 and K % 128 == 0
-    kernel_name = {"gemv": "k_gemv8_mfma" if mfma8 else "k_gemv_tile",
+    # the library's GEMV dispatch: 5..8 vectors (4-bit rows up to 8192 long:
+    # 3..8) over >= 4096 rows run on the matrix cores
+    mfma = (kind == "gemv" and N >= 4096 and K % 128 == 0 and
+            (5 <= batch <= 8 or (bits == 4 and 3 <= batch <= 4 and K <= 8192)))
+    kernel_name = {"gemv": f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile",
                    "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
                    "gemm": "k_gemm_w4" if bits == 4 else "k_gemm"}[kind]
     roof["kernel"] = kernel_name

@@ -1,31 +1,40 @@
-// gemv_mfma.hpp -- 8-bit palettized GEMV for several batch vectors on the
-// matrix cores.
+// gemv_mfma.hpp -- palettized GEMV for several batch vectors on the matrix
+// cores, 4- and 8-bit.
 //
-// y[b, n] = f16( sum_k f32(x[b, k]) * f32(LUT_n[idx(n, k)]) ): the 8-bit
-// extension of lut_gemv_cpu (compute-core/src/lut/evaluator.rs:21-44; the
+// y[b, n] = f16( sum_k f32(x[b, k]) * f32(LUT_n[idx(n, k)]) ): lut_gemv_cpu
+// (compute-core/src/lut/evaluator.rs:21-44) and its 8-bit extension (the
 // format of compute-core/tests/palettized_vs_direct.rs:108-135 laid out
 // split-block), fp32 accumulation, fp16 output.
 //
-// With several batch vectors the VALU kernel spends 2 to 4 v_dot2 per weight
-// element; here v_mfma_f32_16x16x32_f16 does the products (batch vectors are
-// the A rows, padded to 16 with zeros; weight rows the B columns) and each
-// element costs one LDS lookup:
-//  * a workgroup owns 32 weight rows (two 16-column tiles) and their
-//    256-entry fp16 LUTs in LDS (16 KB, entry b of row r at 2 (256 r + b));
-//  * its waves split K into 128-wide groups (group g to wave g % W); lane
-//    (n = lane % 16, kq = lane / 16) supplies, in MFMA step s of a group at
-//    k0, the elements k0 + 32 kq + 8 s .. +7 -- A and B only need to agree
-//    on which k a lane and register hold -- so a lane reads 32 contiguous
-//    index bytes of each of its two rows and 64 contiguous bytes of x per
-//    group, and the next group's loads are in flight while one is looked up;
-//  * the first group is requested before the tables are built;
+// With several batch vectors the VALU kernel spends 2 to 4 v_dot2 per pair
+// of weight elements; here v_mfma_f32_16x16x32_f16 does the products (batch
+// vectors are the A rows, padded to 16 with zeros; weight rows the B
+// columns) and the lookups are all that is left per element:
+//  * a workgroup owns 32 weight rows (two 16-column tiles); its waves split
+//    K into 128-wide groups (group g to wave g % W);
+//  * lane (n = lane % 16, kq = lane / 16) supplies, in MFMA step s of a
+//    group at k0, the elements k0 + 32 kq + 8 s .. +7 -- A and B only need
+//    to agree on which k a lane and register hold -- so a lane reads 32
+//    contiguous elements' index bytes of each of its two rows and 64
+//    contiguous bytes of x per group, and the next group's loads are in
+//    flight while one is looked up; the first group is requested before the
+//    tables are built;
+//  * 8-bit: each row's 256-entry fp16 LUT in LDS (16 KB, entry b of row r at
+//    2 (256 r + b)), one 16-bit lookup per element;
+//  * 4-bit: each row's pair table, entry b = LUT[b & 15] | LUT[b >> 4] << 16
+//    (one index byte -> the fp16 pair of two elements), laid out
+//    [tile][entry][row] (entry b of tile row n at dword 4096 t + 16 b + n):
+//    the four lanes of a row read banks n, n + 16, n + 32, n + 48 by b % 4,
+//    so only lanes of one row can conflict; one dword lookup per two
+//    elements (32 KB);
 //  * the waves' partial tiles are added in LDS and rounded once.
-// The lookups are random reads of a shared table and cost about 7 LDS
-// cycles per wave instruction in bank conflicts; a bank-private layout
-// (each lane's row copied into its own bank, 64 KB for 32 rows with a
-// 32x32 MFMA tile) removes the conflicts but measured slower, its x operand
-// padded to 32 rows and its table build costing more than they save.
-// Requires K % 128 == 0, 16-byte aligned x, nb <= 8 and N * K below 2 GiB.
+// The lookups are random reads of shared tables and cost LDS cycles in bank
+// conflicts; a bank-private layout (each lane's row copied into its own
+// bank, 64 KB for 32 8-bit rows with a 32x32 MFMA tile) removes them but
+// measured slower, its x operand padded to 32 rows and its table build
+// costing more than they save.
+// Requires K % 128 == 0, 16-byte aligned x, nb <= 8 and N * K * BITS / 8
+// below 2 GiB.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -37,16 +46,20 @@ namespace prism {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kG8Tiles = 2;   // 16-row MFMA tiles per workgroup
-constexpr int kG8Rows = 16 * kG8Tiles;
-constexpr int kG8Waves = 8;   // waves splitting K
-constexpr int kG8MaxNb = 8;
-constexpr int kG8Group = 128; // K elements per wave per loop trip (4 MFMA steps)
+constexpr int kGmTiles = 2;   // 16-row MFMA tiles per workgroup
+constexpr int kGmRows = 16 * kGmTiles;
+constexpr int kGmWaves = 8;   // waves splitting K
+constexpr int kGmMaxNb = 8;
+constexpr int kGmGroup = 128; // K elements per wave per loop trip (4 MFMA steps)
 
-__global__ __launch_bounds__(64 * kG8Waves) void k_gemv8_mfma(GemvArgs a) {
-  constexpr int T = kG8Tiles, RN = kG8Rows, KW = kG8Waves;
-  __shared__ __attribute__((aligned(16))) uint16_t tbl[RN * 256];
-  __shared__ float red[KW][RN][kG8MaxNb];
+template <int BITS>
+__global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
+  static_assert(BITS == 4 || BITS == 8, "4- or 8-bit indices");
+  constexpr int T = kGmTiles, RN = kGmRows, KW = kGmWaves, NT = 64 * kGmWaves;
+  constexpr int IB = 32 * BITS / 8;  // index bytes per lane, row and group
+  // 8-bit: [row][256] fp16; 4-bit: [tile][256][16] pair dwords
+  __shared__ __attribute__((aligned(16))) uint32_t tbl[BITS == 8 ? RN * 128 : T * 4096];
+  __shared__ float red[KW][RN][kGmMaxNb];
 
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar buffer offsets
@@ -55,46 +68,57 @@ __global__ __launch_bounds__(64 * kG8Waves) void k_gemv8_mfma(GemvArgs a) {
 
   const uint32_t n = lane & 15, kq = lane >> 4;
   typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2v_t __attribute__((ext_vector_type(2)));
   // x: batch row n of the A operand; rows past nb fall outside the range
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(nb * K * 2u), kBufferWord3);
   const __amdgpu_buffer_rsrc_t ri =
-      __builtin_amdgcn_make_buffer_rsrc((void*)a.idx, (short)0, (int)(N * K), kBufferWord3);
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.idx, (short)0, (int)(N * (K * BITS / 8)), kBufferWord3);
   const uint32_t xv = n * K * 2u + kq * 64u;
   uint32_t iv[T];
 #pragma unroll
   for (int t = 0; t < T; t++) {
     const uint32_t r = n0 + 16 * t + n;
-    iv[t] = (r < N ? r : N - 1) * K + kq * 32u;
+    iv[t] = (r < N ? r : N - 1) * (K * BITS / 8) + kq * IB;
   }
 
   struct Group {
     u32x4v_t x[4];
-    u32x4v_t w[T][2];
+    u32x4v_t w[T][IB / 16];
   };
   auto load = [&](uint32_t g, Group& d) {
-    const uint32_t k0 = (wave + KW * g) * kG8Group;
+    const uint32_t k0 = (wave + KW * g) * kGmGroup;
 #pragma unroll
     for (int j = 0; j < 4; j++) d.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xv + 16 * j, k0 * 2u, 0);
 #pragma unroll
     for (int t = 0; t < T; t++)
 #pragma unroll
-      for (int j = 0; j < 2; j++)
-        d.w[t][j] = __builtin_amdgcn_raw_buffer_load_b128(ri, iv[t] + 16 * j, k0, kNontemporal);
+      for (int j = 0; j < IB / 16; j++)
+        d.w[t][j] = __builtin_amdgcn_raw_buffer_load_b128(ri, iv[t] + 16 * j, k0 * BITS / 8, kNontemporal);
   };
-  // 8 lookups into one row's table
-  auto look8 = [](const uint16_t* tb, uint32_t lo, uint32_t hi) {
-    const _Float16* th = reinterpret_cast<const _Float16*>(tb);
-    half8_t b;
-    b[0] = th[lo & 0xFFu];
-    b[1] = th[(lo >> 8) & 0xFFu];
-    b[2] = th[(lo >> 16) & 0xFFu];
-    b[3] = th[lo >> 24];
-    b[4] = th[hi & 0xFFu];
-    b[5] = th[(hi >> 8) & 0xFFu];
-    b[6] = th[(hi >> 16) & 0xFFu];
-    b[7] = th[hi >> 24];
-    return b;
+  // B operand of tile t: the 8 elements whose index bits are `w`
+  auto lookb = [&](int t, u32x2v_t w) {
+    if constexpr (BITS == 8) {
+      const _Float16* th = reinterpret_cast<const _Float16*>(tbl) + (16 * t + n) * 256;
+      half8_t b;
+      b[0] = th[w.x & 0xFFu];
+      b[1] = th[(w.x >> 8) & 0xFFu];
+      b[2] = th[(w.x >> 16) & 0xFFu];
+      b[3] = th[w.x >> 24];
+      b[4] = th[w.y & 0xFFu];
+      b[5] = th[(w.y >> 8) & 0xFFu];
+      b[6] = th[(w.y >> 16) & 0xFFu];
+      b[7] = th[w.y >> 24];
+      return b;
+    } else {
+      const uint32_t* tt = tbl + 4096 * t + n;
+      u32x4v_t b;
+      b[0] = tt[16 * (w.x & 0xFFu)];
+      b[1] = tt[16 * ((w.x >> 8) & 0xFFu)];
+      b[2] = tt[16 * ((w.x >> 16) & 0xFFu)];
+      b[3] = tt[16 * (w.x >> 24)];
+      return __builtin_bit_cast(half8_t, b);
+    }
   };
   floatx4 acc[T];
 #pragma unroll
@@ -103,33 +127,56 @@ __global__ __launch_bounds__(64 * kG8Waves) void k_gemv8_mfma(GemvArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
       const half8_t av = __builtin_bit_cast(half8_t, d.x[s]);
-      const int h = s >> 1, q = 2 * (s & 1);
 #pragma unroll
-      for (int t = 0; t < T; t++)
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, look8(tbl + (16 * t + n) * 256, d.w[t][h][q],
-                                                                  d.w[t][h][q + 1]),
-                                                        acc[t], 0, 0, 0);
+      for (int t = 0; t < T; t++) {
+        u32x2v_t w;
+        if constexpr (BITS == 8) {
+          w.x = d.w[t][s >> 1][2 * (s & 1)];
+          w.y = d.w[t][s >> 1][2 * (s & 1) + 1];
+        } else {
+          w.x = d.w[t][0][s];
+          w.y = 0;
+        }
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, lookb(t, w), acc[t], 0, 0, 0);
+      }
     }
   };
 
-  const uint32_t ng = K / kG8Group;
+  const uint32_t ng = K / kGmGroup;
   const uint32_t mine = ng > wave ? (ng - wave + KW - 1) / KW : 0;
   Group ga, gb;
   if (mine > 0) load(0, ga);
 
-  // ---- LUTs of the workgroup's rows (rows past N: zeros).  A raw barrier:
-  // __syncthreads would also wait for the group loads above.
-  {
+  // ---- lookup tables of the workgroup's rows (rows past N: zeros).  Raw
+  // barriers: __syncthreads would also wait for the group loads above.
+  const uint32_t live = N - n0 < (uint32_t)RN ? N - n0 : (uint32_t)RN;
+  if constexpr (BITS == 8) {
     const uint4* src = reinterpret_cast<const uint4*>(a.lut + (size_t)n0 * 512);
     uint4* dst = reinterpret_cast<uint4*>(tbl);
-    const uint32_t live = (N - n0 < (uint32_t)RN ? N - n0 : (uint32_t)RN) * 32;  // uint4 per row: 32
 #pragma unroll
-    for (int i = 0; i < RN * 32 / (64 * KW); i++) {
-      const uint32_t e = tid + 64 * KW * i;
-      dst[e] = e < live ? src[e] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < RN * 32 / NT; i++) {
+      const uint32_t e = tid + NT * i;  // uint4 e of row e / 32
+      dst[e] = e < live * 32 ? src[e] : make_uint4(0, 0, 0, 0);
     }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    // the 32 rows' 16-entry LUTs (1 KB) in the reduction buffer, then the
+    // pair tables from them
+    static_assert(sizeof(red) >= RN * 32, "LUT staging fits the reduction buffer");
+    uint16_t* stage = reinterpret_cast<uint16_t*>(&red[0][0][0]);
+    if (tid < (uint32_t)RN * 2) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.lut + (size_t)n0 * 32);
+      reinterpret_cast<uint4*>(stage)[tid] = tid < live * 2 ? src[tid] : make_uint4(0, 0, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < T * 4096 / NT; i++) {
+      const uint32_t e = tid + NT * i;  // dword 4096 t + 16 b + r
+      const uint32_t r = 16 * (e >> 12) + (e & 15), b = (e >> 4) & 255;
+      tbl[e] = (uint32_t)stage[r * 16 + (b & 15)] | ((uint32_t)stage[r * 16 + (b >> 4)] << 16);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // before the staging copy is overwritten
   }
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   if (mine > 0) {
     uint32_t g = 1;
@@ -155,13 +202,13 @@ __global__ __launch_bounds__(64 * kG8Waves) void k_gemv8_mfma(GemvArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const uint32_t m = 4 * kq + i;
-    if (m < (uint32_t)kG8MaxNb)
+    if (m < (uint32_t)kGmMaxNb)
 #pragma unroll
       for (int t = 0; t < T; t++) red[wave][16 * t + n][m] = acc[t][i];
   }
   __syncthreads();
-  for (uint32_t e = tid; e < (uint32_t)(RN * kG8MaxNb); e += 64 * KW) {
-    const uint32_t r = e / kG8MaxNb, m = e % kG8MaxNb;
+  for (uint32_t e = tid; e < (uint32_t)(RN * kGmMaxNb); e += NT) {
+    const uint32_t r = e / kGmMaxNb, m = e % kGmMaxNb;
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < KW; w++) v += red[w][r][m];

@@ -233,16 +233,20 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
     a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
     void* args[] = {&a};
-    // 8-bit, 5..8 batch vectors, 4096 rows or more: the matrix-core kernel
-    // (gemv_mfma.hpp).  Against the tile kernel on MI355X: 19.6 vs 26.0 us
-    // at 14336x4096 and 8 vectors, 29.8 vs 2 x 20 at 4096x14336, 6.1 vs 7.8
-    // at 4864x896; no faster at 3..4 vectors, slower at 896 rows (28
-    // workgroups).
-    if (bits == 8 && !dual && !epi && chunk >= 5 && N >= 4096 && K % prism::kG8Group == 0 &&
-        (uint64_t)N * K < (1ull << 31) && reinterpret_cast<uintptr_t>(a.x) % 16 == 0) {
+    // Several batch vectors over 4096 rows or more: the matrix-core kernel
+    // (gemv_mfma.hpp), from 5 vectors, and for 4-bit rows up to 8192 long
+    // from 3.  Against the tile kernel on MI355X: 4-bit 14336x4096 at 8 / 4
+    // / 3 vectors 11.2 / 10.0 / 9.9 vs 21.8 / 13.3 / 12.9 us; 8-bit at 8
+    // vectors 19.6 vs 26.0 us, 29.8 vs 2 x 20 at 4096x14336, 6.1 vs 7.8 at
+    // 4864x896.  Slower with fewer rows (2048: 64 workgroups), for 8-bit at
+    // 3..4 vectors and for long 4-bit rows at 3..4 (4096x14336: 16.5 vs 14.8).
+    const bool mfma_batch = chunk >= 5 || (bits == 4 && chunk >= 3 && K <= 8192);
+    if (!dual && !epi && mfma_batch && N >= 4096 && K % prism::kGmGroup == 0 &&
+        (uint64_t)N * K * bits / 8 < (1ull << 31) && reinterpret_cast<uintptr_t>(a.x) % 16 == 0) {
       a.nb = chunk;
-      HIP_TRY(ctx, hipLaunchKernel(reinterpret_cast<const void*>(&prism::k_gemv8_mfma),
-                                   dim3((N + prism::kG8Rows - 1) / prism::kG8Rows), dim3(64 * prism::kG8Waves),
+      const void* fn = bits == 8 ? reinterpret_cast<const void*>(&prism::k_gemv_mfma<8>)
+                                 : reinterpret_cast<const void*>(&prism::k_gemv_mfma<4>);
+      HIP_TRY(ctx, hipLaunchKernel(fn, dim3((N + prism::kGmRows - 1) / prism::kGmRows), dim3(64 * prism::kGmWaves),
                                    args, 0, st));
       b0 += chunk;
       continue;
@@ -290,7 +294,12 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
                 hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
-  if (!fast) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  // Up to 32 rows of X: GEMV passes of 8 vectors stream the weights M / 8
+  // times but fill the GPU; the GEMM's 256-row tiles leave most CUs idle
+  // below 256 rows.  MI355X, 14336x4096: 4-bit M = 8 / 32 / 64 take 11 / 43
+  // / 84 us as GEMVs and 95 / 95 / 96 us as the GEMM; 8-bit M = 32 / 64 77 /
+  // 151 against 94 / 95 us.
+  if (!fast || M <= 32) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
   // 4-bit, K % 64 == 0: the MFMA kernel with register decode and LDS-DMA
   // staging (gemm_kernels.hpp, k_gemm_w4); its buffer descriptors address
   // the index block and one block's X rows with 32-bit ranges.

@@ -72,12 +72,13 @@ def test_gemv_batch(pe, oracle, gpu_ctx, bits, N, K, batch):
 
 
 @pytest.mark.parametrize("bits,N,K,batch", [
-    (8, 14336, 4096, 5), (8, 14336, 4096, 6),   # matrix-core kernel (8-bit, 5..8 vectors, N >= 4096)
-    (8, 4100, 1024, 7),                          # ragged last 32-row workgroup
-    (8, 4096, 14336, 8),                         # long rows on the matrix cores
+    (8, 14336, 4096, 5), (8, 14336, 4096, 6),   # matrix-core kernel (5..8 vectors, N >= 4096)
+    (4, 14336, 4096, 6),
+    (8, 4100, 1024, 7), (4, 4100, 1024, 7),      # ragged last 32-row workgroup
+    (8, 4096, 14336, 8), (4, 4096, 14336, 8),    # long rows on the matrix cores
     (8, 4096, 14336, 13),                        # 8 + 5 vectors: two matrix-core passes
-    (4, 4096, 14336, 8),                         # rows too long for 8 vectors a pass: 4 + 4
-    (8, 2048, 14336, 6),                         # too few rows for the matrix cores: 4 + 2
+    (4, 2048, 14336, 8),                         # too few rows for the matrix cores, rows too long
+    (8, 2048, 14336, 6),                         #   for 8 vectors a tile pass: 4 + 4, 4 + 2
     (4, 64, 20000, 7),                           # 2 + 2 + 2 + 1
 ])
 def test_gemv_batch_wide(pe, oracle, gpu_ctx, bits, N, K, batch):
@@ -94,7 +95,7 @@ def test_gemv_batch_wide(pe, oracle, gpu_ctx, bits, N, K, batch):
 
 
 @pytest.mark.parametrize("bits,N,K", [(4, 4864, 896), (4, 1000, 4096), (8, 700, 4096), (4, 33, 40), (8, 20, 24),
-                                      (8, 4096, 1024)])
+                                      (8, 4096, 1024), (4, 4096, 1024)])
 def test_decode_bit_exact_through_gemv(pe, gpu_ctx, bits, N, K):
     """One-hot x (x = e_k) makes every output the decoded weight itself:
     y[r] = LUT_r[idx(r, k)] exactly, through the GEMV kernel's own decode."""
@@ -149,7 +150,9 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
 @pytest.mark.parametrize("bits,M,N,K", [(4, 64, 256, 512), (4, 77, 200, 96), (8, 40, 130, 256),
                                         (4, 3, 5, 64), (4, 10, 20, 40), (4, 300, 1000, 1024),
                                         # 2, 3 and 5 K steps of 64: every tail of the 3-stage ring
-                                        (4, 40, 300, 128), (4, 70, 260, 192), (4, 257, 513, 320)])
+                                        (4, 40, 300, 128), (4, 70, 260, 192), (4, 257, 513, 320),
+                                        # up to 32 rows: GEMV passes of 8 (matrix-core GEMV at N >= 4096)
+                                        (4, 32, 4096, 512), (8, 20, 4100, 256), (4, 33, 300, 512)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
