@@ -235,12 +235,15 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
     void* args[] = {&a};
     // Several batch vectors over 4096 rows or more: the matrix-core kernel
     // (gemv_mfma.hpp), from 5 vectors, and for 4-bit rows up to 8192 long
-    // from 3.  Against the tile kernel on MI355X: 4-bit 14336x4096 at 8 / 4
-    // / 3 vectors 11.2 / 10.0 / 9.9 vs 21.8 / 13.3 / 12.9 us; 8-bit at 8
-    // vectors 19.6 vs 26.0 us, 29.8 vs 2 x 20 at 4096x14336, 6.1 vs 7.8 at
-    // 4864x896.  Slower with fewer rows (2048: 64 workgroups), for 8-bit at
-    // 3..4 vectors and for long 4-bit rows at 3..4 (4096x14336: 16.5 vs 14.8).
-    const bool mfma_batch = chunk >= 5 || (bits == 4 && chunk >= 3 && K <= 8192);
+    // from 3 (from 2 over 8192 rows or more).  Against the tile kernel on
+    // MI355X: 4-bit 14336x4096 at 8 / 4 / 3 / 2 vectors 11.2 / 10.0 / 9.9 /
+    // 9.6 vs 21.8 / 13.3 / 12.9 / 10.2 us; 8-bit at 8 vectors 19.6 vs 26.0
+    // us, 29.8 vs 2 x 20 at 4096x14336, 6.1 vs 7.8 at 4864x896.  Slower with
+    // fewer rows (2048: 64 workgroups), at one vector (9.5 vs 8.6), for 4-bit
+    // at 2 vectors over 4864 rows (4.1 vs 3.6), for 8-bit at 3..4 vectors and
+    // for long 4-bit rows at 3..4 (4096x14336: 16.5 vs 14.8).
+    const bool mfma_batch =
+        chunk >= 5 || (bits == 4 && K <= 8192 && (chunk >= 3 || (chunk == 2 && N >= 8192)));
     if (!dual && !epi && mfma_batch && N >= 4096 && K % prism::kGmGroup == 0 &&
         (uint64_t)N * K * bits / 8 < (1ull << 31) && reinterpret_cast<uintptr_t>(a.x) % 16 == 0) {
       a.nb = chunk;
