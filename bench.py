@@ -462,10 +462,10 @@ def main() -> int:
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": PMC_TRAFFIC.get((args.workload, batch))}
-    # the library's GEMV dispatch: 5..8 vectors (4-bit rows up to 8192 long:
-    # 3..8, and 2 over >= 8192 rows) over >= 4096 rows run on the matrix cores
+    # the library's GEMV dispatch: 5..16 vectors (4-bit rows up to 8192 long:
+    # 3..16, and 2 over >= 8192 rows) over >= 4096 rows run on the matrix cores
     mfma = (kind == "gemv" and N >= 4096 and K % 128 == 0 and
-            (5 <= batch <= 8 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
+            (5 <= batch <= 16 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
     kernel_name = {"gemv": f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile",
                    "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
                    "gemm": "k_gemm_w4" if bits == 4 else "k_gemm"}[kind]

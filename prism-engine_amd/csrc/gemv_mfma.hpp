@@ -8,7 +8,7 @@
 //
 // With several batch vectors the VALU kernel spends 2 to 4 v_dot2 per pair
 // of weight elements; here v_mfma_f32_16x16x32_f16 does the products (batch
-// vectors are the A rows, padded to 16 with zeros; weight rows the B
+// vectors are the A rows, up to 16, padded with zeros; weight rows the B
 // columns) and the lookups are all that is left per element:
 //  * a workgroup owns 32 weight rows (two 16-column tiles); its waves split
 //    K into 128-wide groups (group g to wave g % W);
@@ -33,7 +33,7 @@
 // bank, 64 KB for 32 8-bit rows with a 32x32 MFMA tile) removes them but
 // measured slower, its x operand padded to 32 rows and its table build
 // costing more than they save.
-// Requires K % 128 == 0, 16-byte aligned x, nb <= 8 and N * K * BITS / 8
+// Requires K % 128 == 0, 16-byte aligned x, nb <= 16 and N * K * BITS / 8
 // below 2 GiB.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -49,7 +49,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kGmTiles = 2;   // 16-row MFMA tiles per workgroup
 constexpr int kGmRows = 16 * kGmTiles;
 constexpr int kGmWaves = 8;   // waves splitting K
-constexpr int kGmMaxNb = 8;
+constexpr int kGmMaxNb = 16;  // batch vectors per pass: the A operand's 16 rows
 constexpr int kGmGroup = 128; // K elements per wave per loop trip (4 MFMA steps)
 
 template <int BITS>
@@ -202,9 +202,8 @@ __global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const uint32_t m = 4 * kq + i;
-    if (m < (uint32_t)kGmMaxNb)
 #pragma unroll
-      for (int t = 0; t < T; t++) red[wave][16 * t + n][m] = acc[t][i];
+    for (int t = 0; t < T; t++) red[wave][16 * t + n][m] = acc[t][i];
   }
   __syncthreads();
   for (uint32_t e = tid; e < (uint32_t)(RN * kGmMaxNb); e += NT) {

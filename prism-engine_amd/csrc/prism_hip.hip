@@ -230,6 +230,7 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
   a.xpart = xpart;
   for (uint32_t b0 = 0; b0 < nb;) {
     uint32_t chunk = (nb - b0 < 8) ? nb - b0 : 8;
+    const uint32_t wide = (nb - b0 < (uint32_t)prism::kGmMaxNb) ? nb - b0 : (uint32_t)prism::kGmMaxNb;
     a.x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
     a.y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
     void* args[] = {&a};
@@ -242,10 +243,12 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
     // fewer rows (2048: 64 workgroups), at one vector (9.5 vs 8.6), for 4-bit
     // at 2 vectors over 4864 rows (4.1 vs 3.6), for 8-bit at 3..4 vectors and
     // for long 4-bit rows at 3..4 (4096x14336: 16.5 vs 14.8).
+    // It takes up to 16 vectors a pass, the tile kernel 8.
     const bool mfma_batch =
-        chunk >= 5 || (bits == 4 && K <= 8192 && (chunk >= 3 || (chunk == 2 && N >= 8192)));
+        wide >= 5 || (bits == 4 && K <= 8192 && (wide >= 3 || (wide == 2 && N >= 8192)));
     if (!dual && !epi && mfma_batch && N >= 4096 && K % prism::kGmGroup == 0 &&
         (uint64_t)N * K * bits / 8 < (1ull << 31) && reinterpret_cast<uintptr_t>(a.x) % 16 == 0) {
+      chunk = wide;
       a.nb = chunk;
       const void* fn = bits == 8 ? reinterpret_cast<const void*>(&prism::k_gemv_mfma<8>)
                                  : reinterpret_cast<const void*>(&prism::k_gemv_mfma<4>);
@@ -297,12 +300,12 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
                 hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
-  // Up to 32 rows of X: GEMV passes of 8 vectors stream the weights M / 8
-  // times but fill the GPU; the GEMM's 256-row tiles leave most CUs idle
-  // below 256 rows.  MI355X, 14336x4096: 4-bit M = 8 / 32 / 64 take 11 / 43
-  // / 84 us as GEMVs and 95 / 95 / 96 us as the GEMM; 8-bit M = 32 / 64 77 /
-  // 151 against 94 / 95 us.
-  if (!fast || M <= 32) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  // Up to 64 rows of X: GEMV passes of up to 16 vectors stream the weights
+  // M / 16 times but fill the GPU; the GEMM's 256-row tiles leave most CUs
+  // idle below 256 rows.  MI355X, 14336x4096: 4-bit M = 8 / 32 / 64 / 128
+  // take 11 / 28 / 57 / 113 us as GEMVs and 95 / 95 / 96 / 98 us as the
+  // GEMM; 8-bit M = 64 / 128: 85 / 171 against 95 / 99 us.
+  if (!fast || M <= 64) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
   // 4-bit, K % 64 == 0: the MFMA kernel with register decode and LDS-DMA
   // staging (gemm_kernels.hpp, k_gemm_w4); its buffer descriptors address
   // the index block and one block's X rows with 32-bit ranges.

@@ -76,7 +76,9 @@ def test_gemv_batch(pe, oracle, gpu_ctx, bits, N, K, batch):
     (4, 14336, 4096, 6),
     (8, 4100, 1024, 7), (4, 4100, 1024, 7),      # ragged last 32-row workgroup
     (8, 4096, 14336, 8), (4, 4096, 14336, 8),    # long rows on the matrix cores
-    (8, 4096, 14336, 13),                        # 8 + 5 vectors: two matrix-core passes
+    (8, 4096, 14336, 13),                        # up to 16 vectors a matrix-core pass
+    (4, 14336, 4096, 16), (4, 4096, 1024, 19),   # 16 + 3
+    (8, 4100, 1024, 20),                         # 16 + 4: the 4 by the tile kernel
     (4, 2048, 14336, 8),                         # too few rows for the matrix cores, rows too long
     (8, 2048, 14336, 6),                         #   for 8 vectors a tile pass: 4 + 4, 4 + 2
     (4, 64, 20000, 7),                           # 2 + 2 + 2 + 1
@@ -151,8 +153,8 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
                                         (4, 3, 5, 64), (4, 10, 20, 40), (4, 300, 1000, 1024),
                                         # 2, 3 and 5 K steps of 64: every tail of the 3-stage ring
                                         (4, 40, 300, 128), (4, 70, 260, 192), (4, 257, 513, 320),
-                                        # up to 32 rows: GEMV passes of 8 (matrix-core GEMV at N >= 4096)
-                                        (4, 32, 4096, 512), (8, 20, 4100, 256), (4, 33, 300, 512)])
+                                        # up to 64 rows: GEMV passes of up to 16 (matrix cores at N >= 4096)
+                                        (4, 64, 4096, 512), (8, 20, 4100, 256), (4, 65, 300, 512)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
