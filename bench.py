@@ -330,7 +330,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="hero", choices=sorted(WORKLOADS))
-    ap.add_argument("--batch", type=int, default=None, help="batch for gemv workloads (cfg4 sweep)")
+    ap.add_argument("--batch", type=int, default=None,
+                    help="batch for gemv workloads (cfg4 sweep), rows of X (M) for the GEMM")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes the steps rotate over")
@@ -353,8 +354,8 @@ def main() -> int:
         return run_decode(args, pe, pe.SEEDS.get(args.workload, 1003))
     if kind == "palettize":
         return run_palettize(args, pe, pe.SEEDS.get(args.workload, 1006))
-    if args.batch is not None and kind == "gemv":
-        batch = args.batch
+    if args.batch is not None and kind in ("gemv", "gemm"):
+        batch = args.batch  # batch vectors, or the GEMM's rows of X
     seed = pe.SEEDS.get(args.workload, 1000)
 
     log(f"[bench] workload={args.workload} kind={kind} bits={bits} N={N} K={K} batch/M={batch} seed={seed}")
@@ -468,7 +469,8 @@ def main() -> int:
             (5 <= batch <= 16 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
     kernel_name = {"gemv": f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile",
                    "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
-                   "gemm": "k_gemm_w4" if bits == 4 else "k_gemm"}[kind]
+                   "gemm": (f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" if batch > 48 else
+                            "GEMV passes") if bits == 4 else "k_gemm"}[kind]
     roof["kernel"] = kernel_name
     roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb
 

@@ -184,7 +184,6 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ lut, c
     }
 }
 
-constexpr int GW4_BM = 256;
 constexpr int GW4_BN = 256;
 constexpr int GW4_BK = 64;
 constexpr int GW4_PITCH = GW4_BK + 8;  // halves per LDS row (144 B)
@@ -239,9 +238,7 @@ constexpr int kGwdWord3 = 0x00020000;
 // 256 * K * 2 bytes of X per block below 2 GiB (the buffer descriptors'
 // 32-bit ranges; rows past M or N read as 0 through the range check).
 constexpr int GWD_STAGES = 3;
-constexpr int GWD_XSLOTS = GW4_BM * GW4_BK / 8;  // 16-byte X slots per stage
-constexpr int GWD_WSLOTS = GW4_BN * 2;           // 16-byte index slots per stage
-constexpr int GWD_SLOTS = GWD_XSLOTS + GWD_WSLOTS;
+constexpr int GWD_WSLOTS = GW4_BN * 2;  // 16-byte index slots per stage
 
 __device__ __forceinline__ void gwd_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
@@ -264,11 +261,19 @@ __device__ __forceinline__ void gwd_wait_vm() {
   __builtin_amdgcn_s_waitcnt((N_ & 0xF) | ((N_ >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// MI = 32-row M subtiles per block (BM = 32 MI): 8 for long prefills; 2 and
+// 4 give short ones (65..1024 rows) more blocks.
+template <int MI>
 __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                  const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
                                                  uint32_t N, uint32_t K) {
-  constexpr int BM = GW4_BM, BN = GW4_BN, BK = GW4_BK, S = GWD_STAGES, SL = GWD_SLOTS, XS = GWD_XSLOTS;
-  constexpr int OPS = 10;  // DMA instructions per wave per K step (8 X + 2 index)
+  static_assert(MI == 2 || MI == 4 || MI == 8, "32-row M subtiles per block");
+  constexpr int BM = 32 * MI, BN = GW4_BN, BK = GW4_BK, S = GWD_STAGES;
+  constexpr int XS = BM * BK / 8;     // 16-byte X slots per stage
+  constexpr int SL = XS + GWD_WSLOTS;
+  constexpr int OPS = MI + 2;         // DMA instructions per wave per K step (MI X + 2 index)
+  constexpr int XR = 8 * MI;          // X rows each wave fetches
+  constexpr int VPI = 56 / MI;        // decode VALU ops scheduled per M subtile (2 MFMAs)
   __shared__ __attribute__((aligned(16))) uint4 sx[S * SL];
 
   const int tid = threadIdx.x;
@@ -306,24 +311,24 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   const __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc((void*)idx, (short)0, (int)(N * row_bytes), kGwdWord3);
   const uint32_t lr8 = (uint32_t)lane >> 3, lc = ((uint32_t)lane & 7u) ^ lr8;
-  const uint32_t xv0 = (64u * wave + lr8) * K * 2u + 16u * lc;  // even DMA index
+  const uint32_t xv0 = ((uint32_t)XR * wave + lr8) * K * 2u + 16u * lc;  // even DMA index
   const uint32_t xv1 = xv0 ^ 16u;                                // odd: chunk lc ^ 1
   const uint32_t wv = (n0 + 64u * wave + ((uint32_t)lane >> 1)) * row_bytes + 16u * ((uint32_t)lane & 1u);
 
   auto issue = [&](uint32_t it, int stage) {
     uint4* st = sx + stage * SL;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      gwd_dma16(rx, st + 64 * (8 * wave + i), (i & 1) ? xv1 : xv0, (uint32_t)i * 16u * K + it * 128u);
+    for (int i = 0; i < MI; i++)
+      gwd_dma16(rx, st + 64 * (MI * wave + i), (i & 1) ? xv1 : xv0, (uint32_t)i * 16u * K + it * 128u);
 #pragma unroll
     for (int i = 0; i < 2; i++)
       gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv, (uint32_t)i * 32u * row_bytes + it * 32u);
   };
   auto wdword = [](const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; };
 
-  floatx16 acc[8][2];
+  floatx16 acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int s = 0; s < 2; s++)
 #pragma unroll
@@ -336,14 +341,14 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   const uint32_t asw = ((uint32_t)j & 7u) ^ (((uint32_t)j >> 3) & 1u);
   const uint32_t wsl = 2u * (64u * wave + j) + h;
 
-  half8_t a[2][8];
+  half8_t a[2][MI];
   half8_t bop[2][2];
   uint4 wch[2];
   auto read_first = [&](const uint4* st) {  // index chunks + MFMA step 0's A fragments
     wch[0] = st[XS + wsl];
     wch[1] = st[XS + wsl + 64];
 #pragma unroll
-    for (int i = 0; i < 8; i++) a[0][i] = __builtin_bit_cast(half8_t, st[256 * i + arow + ((4u * h) ^ asw)]);
+    for (int i = 0; i < MI; i++) a[0][i] = __builtin_bit_cast(half8_t, st[256 * i + arow + ((4u * h) ^ asw)]);
   };
   auto decode_b = [&](int buf, int q) {
     bop[buf][0] = decode_nib8_nat(wdword(wch[0], q), pl[0]);
@@ -372,21 +377,21 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     for (int q = 0; q < 3; q++) {
       const int cur = q & 1, nxt = cur ^ 1;
 #pragma unroll
-      for (int i = 0; i < 8; i++)
+      for (int i = 0; i < MI; i++)
         a[nxt][i] = __builtin_bit_cast(half8_t, st[256 * i + arow + ((4u * h + q + 1) ^ asw)]);
       decode_b(nxt, q + 1);
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < MI; i++) {
         acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], bop[cur][0], acc[i][0], 0, 0, 0);
         acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], bop[cur][1], acc[i][1], 0, 0, 0);
       }
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < MI; i++) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, (VPI + 1) / 2, 0);  // VALU
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, VPI / 2, 0);  // VALU
       }
     }
     // MFMA step 3 (operands in buffer 1).  Its B decode, issued under step
@@ -407,7 +412,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
       wch[1] = sn[XS + wsl + 64];
     }
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < MI; i++) {
       if (more) a[0][i] = __builtin_bit_cast(half8_t, sn[256 * i + arow + ((4u * h) ^ asw)]);
       acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1][i], bop[1][0], acc[i][0], 0, 0, 0);
       acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1][i], bop[1][1], acc[i][1], 0, 0, 0);
@@ -415,7 +420,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     if (more) decode_b(0, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read: index chunks
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < MI; i++) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
     }
@@ -435,7 +440,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     const uint32_t n = n0 + 64 * wave + 32 * s + j;
     uint16_t* yc = Y + n;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const uint32_t m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);

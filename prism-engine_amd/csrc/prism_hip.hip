@@ -300,26 +300,32 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
                 hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
-  // Up to 64 rows of X: GEMV passes of up to 16 vectors stream the weights
-  // M / 16 times but fill the GPU; the GEMM's 256-row tiles leave most CUs
-  // idle below 256 rows.  MI355X, 14336x4096: 4-bit M = 8 / 32 / 64 / 128
-  // take 11 / 28 / 57 / 113 us as GEMVs and 95 / 95 / 96 / 98 us as the
-  // GEMM; 8-bit M = 64 / 128: 85 / 171 against 95 / 99 us.
-  if (!fast || M <= 64) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  // Up to 48 rows of X: GEMV passes of up to 16 vectors stream the weights
+  // M / 16 times but take less than the GEMM's fixed cost.  MI355X,
+  // 14336x4096 4-bit: M = 8 / 32 / 48 / 64 take 11 / 28 / 43 / 57 us as
+  // GEMVs and about 53 us as the GEMM with 64-row blocks.
+  if (!fast || M <= 48) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
   // 4-bit, K % 64 == 0: the MFMA kernel with register decode and LDS-DMA
   // staging (gemm_kernels.hpp, k_gemm_w4); its buffer descriptors address
-  // the index block and one block's X rows with 32-bit ranges.
+  // the index block and one block's X rows with 32-bit ranges.  Blocks of
+  // 32 * mi rows of X: short prefills take shorter blocks, so that more of
+  // them fill the GPU.  MI355X, 14336x4096, mi = 2 / 4 / 8: M = 128 53.8 /
+  // 67.8 / 106.2 us, M = 256 63.7 / 71.6 / 108.1, M = 512 110.3 / 89.8 /
+  // 114.6, M = 640 - / 150.7 / 127.7, M = 2048 373.7 / 334.3 / 279.8.
+  const int mi = M <= 256 ? 2 : M <= 512 ? 4 : 8;
+  const uint32_t bm = 32u * (uint32_t)mi;
   if (bits == 4 && K % prism::GW4_BK == 0 && (uint64_t)N * (K / 2) < (1ull << 31) &&
-      (uint64_t)prism::GW4_BM * K * 2 < (1ull << 31)) {
-    const uint32_t tiles4 =
-        ((M + prism::GW4_BM - 1) / prism::GW4_BM) * ((N + prism::GW4_BN - 1) / prism::GW4_BN);
+      (uint64_t)bm * K * 2 < (1ull << 31)) {
+    const uint32_t tiles4 = ((M + bm - 1) / bm) * ((N + prism::GW4_BN - 1) / prism::GW4_BN);
     const uint8_t* lut = w->lut();
     const uint8_t* idx = w->idx();
     const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
     uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
     void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K)};
-    HIP_TRY(ctx, hipLaunchKernel(reinterpret_cast<const void*>(&prism::k_gemm_w4), dim3(tiles4), dim3(256), args, 0,
-                                 st));
+    const void* fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2>)
+                     : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4>)
+                               : reinterpret_cast<const void*>(&prism::k_gemm_w4<8>);
+    HIP_TRY(ctx, hipLaunchKernel(fn, dim3(tiles4), dim3(256), args, 0, st));
     return PRISM_HIP_OK;
   }
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);

@@ -151,10 +151,15 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
 
 @pytest.mark.parametrize("bits,M,N,K", [(4, 64, 256, 512), (4, 77, 200, 96), (8, 40, 130, 256),
                                         (4, 3, 5, 64), (4, 10, 20, 40), (4, 300, 1000, 1024),
-                                        # 2, 3 and 5 K steps of 64: every tail of the 3-stage ring
-                                        (4, 40, 300, 128), (4, 70, 260, 192), (4, 257, 513, 320),
-                                        # up to 64 rows: GEMV passes of up to 16 (matrix cores at N >= 4096)
-                                        (4, 64, 4096, 512), (8, 20, 4100, 256), (4, 65, 300, 512)])
+                                        # 2, 3 and 5 K steps of 64: every tail of the 3-stage ring,
+                                        # with 64-, 128- and 256-row blocks
+                                        (4, 60, 300, 128), (4, 70, 260, 192), (4, 100, 260, 320),
+                                        (4, 257, 513, 320), (4, 600, 300, 128), (4, 520, 300, 320),
+                                        # up to 48 rows: GEMV passes of up to 16 (matrix cores at N >= 4096)
+                                        (4, 48, 4096, 512), (8, 20, 4100, 256),
+                                        # 64-, 128- and 256-row blocks (M <= 256, <= 512, more)
+                                        (4, 49, 300, 512), (4, 200, 4100, 256), (4, 300, 700, 192),
+                                        (4, 513, 260, 128)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
