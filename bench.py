@@ -327,8 +327,8 @@ def run_palettize(args, pe, seed) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 2000; palettize: 10)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 50; palettize: 2)")
     ap.add_argument("--workload", default="hero", choices=sorted(WORKLOADS))
     ap.add_argument("--batch", type=int, default=None,
                     help="batch for gemv workloads (cfg4 sweep), rows of X (M) for the GEMM")
@@ -339,6 +339,11 @@ def main() -> int:
                     help="after timing, run one untimed device copy of MB MiB (scale reference for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    # a palettize step compiles a whole model (about 0.1 s)
+    if args.steps is None:
+        args.steps = 10 if args.workload == "palettize" else 2000
+    if args.warmup is None:
+        args.warmup = 2 if args.workload == "palettize" else 50
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

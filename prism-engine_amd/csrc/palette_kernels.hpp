@@ -13,8 +13,9 @@
 // order changes the result, and in parallel only where it cannot:
 //  * k-means++ picks (from channel[n/2], golden-ratio thresholds): the
 //    min-distance update is per element (parallel over lanes); the total is
-//    a sequential fp32 fold in element order (lane 0) that also stores every
-//    partial sum; those partial sums are the reference's cumulative scan, and
+//    a sequential fp32 fold in element order (a chain of adds handed from
+//    lane to lane) that also stores every partial sum; those partial sums are
+//    the reference's cumulative scan, and
 //    since they never decrease (non-negative terms, monotone rounding) the
 //    first one >= the threshold is found by binary search;
 //  * Lloyd iterations: the assignment (first strictly smallest squared
@@ -51,28 +52,46 @@ __host__ __device__ constexpr uint32_t palette_pad(uint32_t n) { return (n + 15u
 // iterations) and partial sums, palette_pad(n) floats each.
 __host__ __device__ constexpr size_t palette_row_bytes(uint32_t n) { return (size_t)palette_pad(n) * 12; }
 
-// Sequential fp32 fold of v[0..np) (np % 16 == 0), storing each partial sum.
-__device__ __forceinline__ float palette_fold_prefix(const float* v, float* pre, uint32_t np) {
-  float s = 0.0f;
-  for (uint32_t i = 0; i < np; i += 16) {
-    float4 t[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) t[q] = reinterpret_cast<const float4*>(v + i)[q];
+// Sequential fp32 fold of v[0..np) (np % 16 == 0) in element order,
+// storing each partial sum; called by the whole wave.  Lane l holds the 16
+// consecutive elements 1024 p + 16 l .. +15 of pass p in registers; the
+// running sum passes from lane to lane (readlane), so the chain of adds runs
+// in registers instead of waiting on an LDS read every 16 elements.  The
+// additions and their order are those of one lane folding v[0], v[1], ...
+__device__ __forceinline__ float palette_fold_prefix(const float* v, float* pre, uint32_t np, uint32_t lane) {
+#pragma clang fp contract(off)
+  float carry = 0.0f;
+  for (uint32_t c0 = 0; c0 < np; c0 += 1024) {
+    const uint32_t base = c0 + 16 * lane;
+    const bool live = base < np;
+    float t[16];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      float4 o;
-      s += t[q].x;
-      o.x = s;
-      s += t[q].y;
-      o.y = s;
-      s += t[q].z;
-      o.z = s;
-      s += t[q].w;
-      o.w = s;
-      reinterpret_cast<float4*>(pre + i)[q] = o;
+      const float4 f = live ? reinterpret_cast<const float4*>(v + base)[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      t[4 * q] = f.x;
+      t[4 * q + 1] = f.y;
+      t[4 * q + 2] = f.z;
+      t[4 * q + 3] = f.w;
+    }
+    const uint32_t lanes = (np - c0) / 16 < 64u ? (np - c0) / 16 : 64u;
+    for (uint32_t l = 0; l < lanes; l++) {
+      if (lane == l) {
+        float s = carry;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          s += t[j];
+          t[j] = s;
+        }
+      }
+      carry = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, t[15]), l));
+    }
+    if (live) {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        reinterpret_cast<float4*>(pre + base)[q] = make_float4(t[4 * q], t[4 * q + 1], t[4 * q + 2], t[4 * q + 3]);
     }
   }
-  return s;
+  return carry;
 }
 
 // Index of the first entry of the non-decreasing pre[0..n) that is >= t,
@@ -166,8 +185,9 @@ __global__ __launch_bounds__(64) void k_palettize(const float* __restrict__ w, u
       reinterpret_cast<float4*>(md)[b] = m;
     }
     __syncthreads();
+    const float total = palette_fold_prefix(md, pre, np, lane);
+    __syncthreads();
     if (lane == 0) {
-      const float total = palette_fold_prefix(md, pre, np);
       uint32_t pick;
       if (total <= 0.0f) {
         pick = (uint32_t)(((uint64_t)nc * n / k) % n);
@@ -197,11 +217,20 @@ __global__ __launch_bounds__(64) void k_palettize(const float* __restrict__ w, u
     if (lane < k) {
       float acc = 0.0f;
       uint32_t cnt = 0;
+      // block i + 16 is read while block i is folded
+      uint4 an = *reinterpret_cast<const uint4*>(asg4);
+      float4 tn[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) tn[q] = reinterpret_cast<const float4*>(val)[q];
       for (uint32_t i = 0; i < np; i += 16) {
-        const uint4 a = *reinterpret_cast<const uint4*>(asg4 + i / 4);
+        const uint4 a = an;
         float4 t[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) t[q] = reinterpret_cast<const float4*>(val + i)[q];
+        for (int q = 0; q < 4; q++) t[q] = tn[q];
+        const uint32_t inext = i + 16 < np ? i + 16 : i;  // the last block reads itself again
+        an = *reinterpret_cast<const uint4*>(asg4 + inext / 4);
+#pragma unroll
+        for (int q = 0; q < 4; q++) tn[q] = reinterpret_cast<const float4*>(val + inext)[q];
         const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
