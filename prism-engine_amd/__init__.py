@@ -2,9 +2,10 @@
 
 The product is ``libprism_hip.so`` (C ABI: ``include/prism_hip.h``), built
 from ``csrc/``: hand-written HIP kernels for the palettized decode GEMV
-(4/8-bit, batch 1..8), the fused gate_up + SwiGLU GEMV and the prefill GEMM
-(LUT tiles decoded into LDS feeding fp16 MFMA).  This package is the
-host-side mirror of the reference's backend surface over that ABI.
+(4/8-bit, any batch), the fused gate_up + SwiGLU GEMV, the prefill GEMM
+(LUT decode feeding fp16 MFMA), the GPU-resident decode step and the palette
+compiler.  This package is the host-side mirror of the reference's backend
+surface over that ABI.
 
 The directory name is not a Python identifier; import it with
 ``importlib.import_module("prism-engine_amd")``.

@@ -118,7 +118,9 @@ hipStream_t pick_stream(prism_hip_ctx* ctx, void* stream) {
 
 // ---------------------------------------------------------------- GEMV plan
 // k_gemv_tile (gemv_tile.hpp) for K % 8 == 0 with 16-byte aligned x, in
-// passes of up to 8 batch vectors; k_gemv_generic otherwise.
+// passes of up to 8 batch vectors (the matrix-core kernel of gemv_mfma.hpp
+// takes several vectors over many rows, up to 16 a pass); k_gemv_generic
+// otherwise.
 
 struct TilePlan {
   const void* fn = nullptr;
