@@ -474,8 +474,9 @@ def main() -> int:
             (5 <= batch <= 16 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
     kernel_name = {"gemv": f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile",
                    "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
-                   "gemm": (f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" if batch > 48 else
-                            "GEMV passes") if bits == 4 else "k_gemm"}[kind]
+                   "gemm": ("GEMV passes" if batch <= (64 if bits == 8 else 48) else
+                            f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" if bits == 4 else
+                            "k_gemm<8>")}[kind]
     roof["kernel"] = kernel_name
     roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb
 

@@ -302,11 +302,12 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
                 hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
-  // Up to 48 rows of X: GEMV passes of up to 16 vectors stream the weights
-  // M / 16 times but take less than the GEMM's fixed cost.  MI355X,
-  // 14336x4096 4-bit: M = 8 / 32 / 48 / 64 take 11 / 28 / 43 / 57 us as
-  // GEMVs and about 53 us as the GEMM with 64-row blocks.
-  if (!fast || M <= 48) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  // Up to 48 rows of X (64 for 8-bit weights): GEMV passes of up to 16
+  // vectors stream the weights M / 16 times but take less than the GEMM's
+  // fixed cost.  MI355X, 14336x4096 4-bit: M = 8 / 32 / 48 / 64 take 11 / 28
+  // / 43 / 57 us as GEMVs and about 53 us as the GEMM with 64-row blocks;
+  // 8-bit M = 64 / 128: 85 / 171 us against 97 / 100 us.
+  if (!fast || M <= (bits == 8 ? 64u : 48u)) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
   // 4-bit, K % 64 == 0: the MFMA kernel with register decode and LDS-DMA
   // staging (gemm_kernels.hpp, k_gemm_w4); its buffer descriptors address
   // the index block and one block's X rows with 32-bit ranges.  Blocks of

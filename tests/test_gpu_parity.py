@@ -159,7 +159,9 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
                                         (4, 48, 4096, 512), (8, 20, 4100, 256),
                                         # 64-, 128- and 256-row blocks (M <= 256, <= 512, more)
                                         (4, 49, 300, 512), (4, 200, 4100, 256), (4, 300, 700, 192),
-                                        (4, 513, 260, 128)])
+                                        (4, 513, 260, 128),
+                                        # 8-bit: GEMV passes up to 64 rows, the LDS-decode GEMM past them
+                                        (8, 64, 4096, 256), (8, 80, 300, 256)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
