@@ -13,7 +13,8 @@ value = effective weight bytes (index + LUT bytes) x K / timed seconds.
 
 Other workloads (--workload): cfg1 (4-bit 4864x896), cfg2 (gate_up+SwiGLU
 2x18944x3584), cfg4 (8-bit 14336x4096, --batch B), cfg5 (prefill GEMM
-2048x4096x14336, TFLOP/s), cfg3 (one decode step of a random-init
+2048x4096x14336, TFLOP/s; --batch sets M), gemm8 (the cfg5 shape with 8-bit
+weights), cfg3 (one decode step of a random-init
 Qwen2.5-0.5B-architecture model, 4-bit, KV length 512: tokens/s; a step is
 one token, KV rolled back to 512 after each so every step does the same
 work), palettize (the palette compiler: one step palettizes every matrix of
@@ -51,6 +52,7 @@ WORKLOADS = {
     "cfg2": ("gateup", 4, 18944, 3584, 1),
     "cfg4": ("gemv", 8, 14336, 4096, 1),
     "cfg5": ("gemm", 4, 14336, 4096, 2048),
+    "gemm8": ("gemm", 8, 14336, 4096, 2048),  # the cfg5 shape with 8-bit weights (not a BASELINE config)
     "cfg3": ("decode", 4, 0, 0, 1),
     "palettize": ("palettize", 4, 0, 0, 1),
 }
@@ -476,7 +478,7 @@ def main() -> int:
                    "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
                    "gemm": ("GEMV passes" if batch <= (64 if bits == 8 else 48) else
                             f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" if bits == 4 else
-                            "k_gemm<8>")}[kind]
+                            "k_gemm8" if batch > 256 and K % 64 == 0 else "k_gemm<8>")}[kind]
     roof["kernel"] = kernel_name
     roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb
 

@@ -184,6 +184,154 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ lut, c
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_gemm8: 8-bit prefill GEMM.  The LDS-decode scheme of k_gemm (the block's
+// 128 row LUTs in LDS, each K step's index tile decoded through them into
+// an fp16 B tile) with a 256 (M) x 128 (N) block tile and a 64-wide K step:
+// each decoded weight feeds twice the MFMAs, and a step's two barriers cover
+// twice the K.
+//  * 4 waves as 2 (M) x 2 (N): wave (wm, wn) owns rows [128 wm, +128) x
+//    columns [64 wn, +64) = 4 x 2 v_mfma_f32_32x32x16_f16 tiles.
+//  * LDS: LUTs 64 KB, X tile 256 x 64 and B tile 128 x 64 fp16 with a
+//    144-byte row pitch (16 rows at one 16-byte column land in 16 distinct
+//    4-bank groups).
+//  * The next step's global loads are issued before the current step's
+//    MFMAs; blocks are mapped XCD-aware like k_gemm's.
+constexpr int GM8_BM = 256;
+constexpr int GM8_BN = 128;
+constexpr int GM8_BK = 64;
+
+__global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
+                                               const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
+                                               uint32_t N, uint32_t K) {
+  constexpr int BM = GM8_BM, BN = GM8_BN, BK = GM8_BK, P = BK + 8;
+  constexpr int XU = BM * BK / 8 / 256;  // 16-byte X chunks per thread per step (8)
+  constexpr int WU = BN * BK / 16 / 256; // 16-byte index chunks per thread per step (2)
+  __shared__ __attribute__((aligned(16))) uint16_t sA[BM * P];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[BN * P];
+  __shared__ __attribute__((aligned(16))) uint16_t sL[BN * 256];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const uint32_t mt = (M + BM - 1) / BM;
+  const uint32_t nt = (N + BN - 1) / BN;
+  const uint32_t ntiles = mt * nt;
+  uint32_t t = blockIdx.x;
+  {
+    const uint32_t per = ntiles / 8, rem = ntiles % 8;
+    const uint32_t xcd = t % 8, slot = t / 8;
+    const uint32_t start = xcd * per + (xcd < rem ? xcd : rem);
+    const uint32_t cnt = per + (xcd < rem ? 1u : 0u);
+    t = (slot < cnt) ? start + slot : t;
+  }
+  const uint32_t n0 = (t % nt) * BN;
+  const uint32_t m0 = (t / nt) * BM;
+
+  // ---- LUTs of this block's rows -> LDS (rows past N are zero)
+  {
+    constexpr int U4 = BN * 256 * 2 / 16;
+    const uint4* src = reinterpret_cast<const uint4*>(lut + (size_t)n0 * 512);
+    uint4* dst = reinterpret_cast<uint4*>(sL);
+    const uint32_t live_u4 = (N - n0 < (uint32_t)BN ? N - n0 : (uint32_t)BN) * 32;
+    for (int i = tid; i < U4; i += 256) dst[i] = (uint32_t)i < live_u4 ? src[i] : make_uint4(0, 0, 0, 0);
+  }
+
+  // chunk c = tid + 256 i: X row c / 8, column chunk c % 8; index row c / 4, chunk c % 4
+  uint4 ra[XU], rb[WU];
+  auto gload = [&](uint32_t k0) {
+#pragma unroll
+    for (int i = 0; i < XU; i++) {
+      const int c = tid + 256 * i;
+      const uint32_t m = m0 + (c >> 3);
+      ra[i] = (m < M) ? *reinterpret_cast<const uint4*>(X + (size_t)m * K + k0 + 8 * (c & 7)) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < WU; i++) {
+      const int c = tid + 256 * i;
+      const uint32_t n = n0 + (c >> 2);
+      rb[i] = (n < N) ? *reinterpret_cast<const uint4*>(idx + (size_t)n * K + k0 + 16 * (c & 3))
+                      : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int i = 0; i < XU; i++) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<uint4*>(&sA[(c >> 3) * P + 8 * (c & 7)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < WU; i++) {
+      const int c = tid + 256 * i, r = c >> 2;
+      const uint16_t* tb = &sL[r * 256];
+      const uint32_t w4[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+      uint32_t o[8];
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+          const uint32_t lo = tb[(w4[q] >> (16 * p)) & 255u];
+          const uint32_t hi = tb[(w4[q] >> (16 * p + 8)) & 255u];
+          o[2 * q + p] = lo | (hi << 16);
+        }
+      uint4* d = reinterpret_cast<uint4*>(&sB[r * P + 16 * (c & 3)]);
+      d[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+  };
+
+  floatx16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+  const uint32_t nk = K / BK;
+  gload(0);
+  __syncthreads();  // sL ready
+  for (uint32_t ks = 0; ks < nk; ks++) {
+    lstore();
+    __syncthreads();
+    if (ks + 1 < nk) gload((ks + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      half8_t af[4], bf[2];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = wm * 128 + i * 32 + (lane & 31);
+        af[i] = *reinterpret_cast<const half8_t*>(&sA[r * P + kk + 8 * (lane >> 5)]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int r = wn * 64 + j * 32 + (lane & 31);
+        bf[j] = *reinterpret_cast<const half8_t*>(&sB[r * P + kk + 8 * (lane >> 5)]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: D lane layout: col = lane%32, row = 8*(e/4) + 4*(lane/32) + e%4
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const uint32_t n = n0 + wn * 64 + j * 32 + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const uint32_t m = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (m < M && n < N) Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][e]);
+      }
+    }
+}
+
 constexpr int GW4_BN = 256;
 constexpr int GW4_BK = 64;
 constexpr int GW4_PITCH = GW4_BK + 8;  // halves per LDS row (144 B)

@@ -331,6 +331,20 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
     HIP_TRY(ctx, hipLaunchKernel(fn, dim3(tiles4), dim3(256), args, 0, st));
     return PRISM_HIP_OK;
   }
+  // 8-bit, K % 64 == 0, more than 256 rows: 256 x 128 blocks over a 64-wide
+  // K step (k_gemm8).  MI355X, 14336x4096: M = 384 / 512 / 2048 take 118 /
+  // 123 / 454 us against 197 / 206 / 701 us in k_gemm<8>'s 128 x 128 blocks,
+  // which stay ahead up to 256 rows (102 against 112 us).
+  if (bits == 8 && K % prism::GM8_BK == 0 && M > 256) {
+    const uint32_t tiles8 = ((M + prism::GM8_BM - 1) / prism::GM8_BM) * ((N + prism::GM8_BN - 1) / prism::GM8_BN);
+    const uint8_t* lut = w->lut();
+    const uint8_t* idx = w->idx();
+    const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
+    uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
+    void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K)};
+    HIP_TRY(ctx, hipLaunchKernel(reinterpret_cast<const void*>(&prism::k_gemm8), dim3(tiles8), dim3(256), args, 0, st));
+    return PRISM_HIP_OK;
+  }
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
   const uint8_t* lut = w->lut();
   const uint8_t* idx = w->idx();

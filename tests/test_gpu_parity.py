@@ -161,7 +161,10 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
                                         (4, 49, 300, 512), (4, 200, 4100, 256), (4, 300, 700, 192),
                                         (4, 513, 260, 128),
                                         # 8-bit: GEMV passes up to 64 rows, the LDS-decode GEMM past them
-                                        (8, 64, 4096, 256), (8, 80, 300, 256)])
+                                        (8, 64, 4096, 256), (8, 80, 300, 256),
+                                        # 8-bit over 256 rows: 256 x 128 blocks, K step 64; else 128 x 128, step 32
+                                        (8, 300, 1000, 1024), (8, 513, 260, 192), (8, 257, 300, 64),
+                                        (8, 256, 300, 128), (8, 300, 129, 96)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
