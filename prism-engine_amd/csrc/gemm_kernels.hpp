@@ -411,10 +411,13 @@ __device__ __forceinline__ void gwd_wait_vm() {
 
 // MI = 32-row M subtiles per block (BM = 32 MI): 8 for long prefills; 2 and
 // 4 give short ones (65..1024 rows) more blocks.
-template <int MI>
+// SPLIT: block (x, y) covers K steps [y kps, min(K / 64, (y + 1) kps)) and
+// writes its fp32 partial tile to P[y][M][N] (k_gemm_split_sum adds the
+// partials); otherwise the whole K range, fp16 to Y.
+template <int MI, bool SPLIT>
 __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                  const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
-                                                 uint32_t N, uint32_t K) {
+                                                 uint32_t N, uint32_t K, float* __restrict__ P, uint32_t kps) {
   static_assert(MI == 2 || MI == 4 || MI == 8, "32-row M subtiles per block");
   constexpr int BM = 32 * MI, BN = GW4_BN, BK = GW4_BK, S = GWD_STAGES;
   constexpr int XS = BM * BK / 8;     // 16-byte X slots per stage
@@ -441,7 +444,8 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   const uint32_t n0 = (t % nt) * BN;
   const uint32_t m0 = (t / nt) * BM;
   const uint32_t row_bytes = K / 2;
-  const uint32_t nk = K / BK;
+  const uint32_t kb = SPLIT ? blockIdx.y * kps : 0u;  // first K step
+  const uint32_t nk = SPLIT ? (K / BK - kb < kps ? K / BK - kb : kps) : K / BK;
 
   // ---- LUT planes of this lane's two weight rows (rows past N: the last row)
   LutPlanes pl[2];
@@ -467,10 +471,10 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     uint4* st = sx + stage * SL;
 #pragma unroll
     for (int i = 0; i < MI; i++)
-      gwd_dma16(rx, st + 64 * (MI * wave + i), (i & 1) ? xv1 : xv0, (uint32_t)i * 16u * K + it * 128u);
+      gwd_dma16(rx, st + 64 * (MI * wave + i), (i & 1) ? xv1 : xv0, (uint32_t)i * 16u * K + (it + kb) * 128u);
 #pragma unroll
     for (int i = 0; i < 2; i++)
-      gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv, (uint32_t)i * 32u * row_bytes + it * 32u);
+      gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv, (uint32_t)i * 32u * row_bytes + (it + kb) * 32u);
   };
   auto wdword = [](const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; };
 
@@ -587,13 +591,47 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   for (int s = 0; s < 2; s++) {
     const uint32_t n = n0 + 64 * wave + 32 * s + j;
     uint16_t* yc = Y + n;
+    float* pc = SPLIT ? P + (size_t)blockIdx.y * M * N + n : nullptr;
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const uint32_t m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (full || (m < M && n < N)) yc[(size_t)m * N] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][s][e]);
+        if (full || (m < M && n < N)) {
+          if constexpr (SPLIT)
+            pc[(size_t)m * N] = acc[i][s][e];
+          else
+            yc[(size_t)m * N] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][s][e]);
+        }
       }
+  }
+}
+
+// Y[i] = f16(P[0][i] + P[1][i] + ... + P[S-1][i]) over mn = M N elements,
+// the splits added in order in fp32 (deterministic), four elements a thread.
+__global__ __launch_bounds__(256) void k_gemm_split_sum(const float* __restrict__ P, uint16_t* __restrict__ Y,
+                                                        uint64_t mn, uint32_t S) {
+  const uint64_t i0 = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * 4u;
+  if (i0 >= mn) return;
+  if (mn % 4 == 0) {  // i0 + 4 <= mn and every split's row of 4 is 16-byte aligned
+    float4 a = *reinterpret_cast<const float4*>(P + i0);
+    for (uint32_t s = 1; s < S; s++) {
+      const float4 b = *reinterpret_cast<const float4*>(P + s * mn + i0);
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    }
+    Y[i0 + 0] = __builtin_bit_cast(uint16_t, (_Float16)a.x);
+    Y[i0 + 1] = __builtin_bit_cast(uint16_t, (_Float16)a.y);
+    Y[i0 + 2] = __builtin_bit_cast(uint16_t, (_Float16)a.z);
+    Y[i0 + 3] = __builtin_bit_cast(uint16_t, (_Float16)a.w);
+    return;
+  }
+  for (uint64_t i = i0; i < i0 + 4 && i < mn; i++) {
+    float a = P[i];
+    for (uint32_t s = 1; s < S; s++) a += P[s * mn + i];
+    Y[i] = __builtin_bit_cast(uint16_t, (_Float16)a);
   }
 }
 

@@ -33,6 +33,10 @@ struct prism_hip_ctx {
   size_t lds_max = 65536;  // dynamic + static LDS bytes one workgroup may use
   void* d_stage = nullptr;
   size_t stage_bytes = 0;
+  // Stream-ordered pool for per-call device scratch (split-K partials),
+  // created on first use; it keeps what it has allocated, so a call after
+  // the first reuses memory instead of allocating.
+  hipMemPool_t pool = nullptr;
   std::string err;
   // Weights uploaded through this context; destroying the context orphans
   // them (w->ctx = nullptr) so a later prism_hip_weight_free stays valid.
@@ -103,6 +107,26 @@ int ensure_stage(prism_hip_ctx* ctx, size_t bytes) {
   while (sz < bytes) sz <<= 1;
   HIP_TRY(ctx, hipMalloc(&ctx->d_stage, sz));
   ctx->stage_bytes = sz;
+  return PRISM_HIP_OK;
+}
+
+int ensure_pool(prism_hip_ctx* ctx) {
+  if (ctx->pool) return PRISM_HIP_OK;
+  hipMemPoolProps props;
+  std::memset(&props, 0, sizeof props);
+  props.allocType = hipMemAllocationTypePinned;
+  props.handleTypes = hipMemHandleTypeNone;
+  props.location.type = hipMemLocationTypeDevice;
+  props.location.id = ctx->device;
+  hipMemPool_t pool = nullptr;
+  HIP_TRY(ctx, hipMemPoolCreate(&pool, &props));
+  uint64_t keep = UINT64_MAX;  // never trim at synchronisation points
+  const hipError_t e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+  if (e != hipSuccess) {
+    (void)hipMemPoolDestroy(pool);
+    return fail(ctx, PRISM_HIP_ERR_DEVICE, "hipMemPoolSetAttribute: %s", hipGetErrorString(e));
+  }
+  ctx->pool = pool;
   return PRISM_HIP_OK;
 }
 
@@ -302,12 +326,12 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
                 hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
-  // Up to 48 rows of X (64 for 8-bit weights): GEMV passes of up to 16
+  // Up to 32 rows of X (64 for 8-bit weights): GEMV passes of up to 16
   // vectors stream the weights M / 16 times but take less than the GEMM's
-  // fixed cost.  MI355X, 14336x4096 4-bit: M = 8 / 32 / 48 / 64 take 11 / 28
-  // / 43 / 57 us as GEMVs and about 53 us as the GEMM with 64-row blocks;
-  // 8-bit M = 64 / 128: 85 / 171 us against 97 / 100 us.
-  if (!fast || M <= (bits == 8 ? 64u : 48u)) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  // fixed cost.  MI355X, 14336x4096 4-bit: M = 24 / 32 / 40 / 48 take 25.7 /
+  // 28.2 / 38.2 / 41.6 us as GEMVs and 31.1 / 31.5 / 31.9 / 32.8 us as the
+  // split-K GEMM; 8-bit M = 64 / 128: 85 / 171 us against 97 / 100 us.
+  if (!fast || M <= (bits == 8 ? 64u : 32u)) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
   // 4-bit, K % 64 == 0: the MFMA kernel with register decode and LDS-DMA
   // staging (gemm_kernels.hpp, k_gemm_w4); its buffer descriptors address
   // the index block and one block's X rows with 32-bit ranges.  Blocks of
@@ -315,7 +339,29 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
   // them fill the GPU.  MI355X, 14336x4096, mi = 2 / 4 / 8: M = 128 53.8 /
   // 67.8 / 106.2 us, M = 256 63.7 / 71.6 / 108.1, M = 512 110.3 / 89.8 /
   // 114.6, M = 640 - / 150.7 / 127.7, M = 2048 373.7 / 334.3 / 279.8.
-  const int mi = M <= 256 ? 2 : M <= 512 ? 4 : 8;
+  // Short 4-bit prefills split K: a block decodes its 256 weight rows over
+  // its K range whatever its M rows, so up to 256 rows of X one M block of
+  // 128 or 256 rows takes the whole GPU in K splits (at most 4, at least 8
+  // K steps each; fp32 partials from the context's stream-ordered pool,
+  // added in split order by k_gemm_split_sum).  MI355X, 14336x4096, M = 64 /
+  // 128 / 192 / 256: 33.3 / 37.4 / 53.4 / 57.0 us against 52.6 / 54.6 / 58.9
+  // / 65.6 unsplit; two splits, or 64-row blocks, came between; at 384 and
+  // 512 rows splitting lost (88.7 / 94.1 against 79.9 / 89.6 us).
+  const uint32_t nsteps = K / prism::GW4_BK;
+  const uint32_t ntn = (N + prism::GW4_BN - 1) / prism::GW4_BN;
+  uint32_t nsplit = 1;
+  int mi = M <= 256 ? 2 : M <= 512 ? 4 : 8;
+  if (M <= 256) {
+    const int smi = M <= 128 ? 4 : 8;
+    const uint32_t blocks = ((M + 32u * smi - 1) / (32u * smi)) * ntn;
+    uint32_t sk = (uint32_t)ctx->num_cu / blocks;
+    sk = sk < 4 ? sk : 4;
+    sk = sk < nsteps / 8 ? sk : nsteps / 8;
+    if (sk >= 2) {
+      nsplit = sk;
+      mi = smi;
+    }
+  }
   const uint32_t bm = 32u * (uint32_t)mi;
   if (bits == 4 && K % prism::GW4_BK == 0 && (uint64_t)N * (K / 2) < (1ull << 31) &&
       (uint64_t)bm * K * 2 < (1ull << 31)) {
@@ -324,11 +370,38 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
     const uint8_t* idx = w->idx();
     const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
     uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
-    void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K)};
-    const void* fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2>)
-                     : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4>)
-                               : reinterpret_cast<const void*>(&prism::k_gemm_w4<8>);
-    HIP_TRY(ctx, hipLaunchKernel(fn, dim3(tiles4), dim3(256), args, 0, st));
+    const bool split = nsplit > 1;
+    float* P = nullptr;
+    uint32_t kps = 0, ns = 1;
+    if (split) {
+      kps = (nsteps + nsplit - 1) / nsplit;
+      ns = (nsteps + kps - 1) / kps;  // every split has at least one K step
+      int rc = ensure_pool(ctx);
+      if (rc) return rc;
+      HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), (size_t)ns * M * N * 4, ctx->pool, st));
+    }
+    void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K), &P, &kps};
+    const void* fn;
+    if (split)
+      fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2, true>)
+           : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4, true>)
+                     : reinterpret_cast<const void*>(&prism::k_gemm_w4<8, true>);
+    else
+      fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2, false>)
+           : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4, false>)
+                     : reinterpret_cast<const void*>(&prism::k_gemm_w4<8, false>);
+    hipError_t e = hipLaunchKernel(fn, dim3(tiles4, ns), dim3(256), args, 0, st);
+    if (e == hipSuccess && split) {
+      const uint64_t mn = (uint64_t)M * N;
+      hipLaunchKernelGGL(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y, mn,
+                         ns);
+      e = hipGetLastError();
+    }
+    if (split) {
+      const hipError_t f = hipFreeAsync(P, st);
+      if (e == hipSuccess) e = f;
+    }
+    if (e != hipSuccess) return fail(ctx, PRISM_HIP_ERR_DEVICE, "GEMM launch: %s", hipGetErrorString(e));
     return PRISM_HIP_OK;
   }
   // 8-bit, K % 64 == 0, more than 256 rows: 256 x 128 blocks over a 64-wide
@@ -439,6 +512,10 @@ void prism_hip_ctx_destroy(prism_hip_ctx* ctx) {
     (void)hipStreamDestroy(ctx->stream);
   }
   if (ctx->d_stage) (void)hipFree(ctx->d_stage);
+  if (ctx->pool) {
+    (void)hipDeviceSynchronize();  // scratch freed on other streams
+    (void)hipMemPoolDestroy(ctx->pool);
+  }
   delete ctx;
 }
 

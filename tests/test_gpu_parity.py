@@ -164,7 +164,11 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
                                         (8, 64, 4096, 256), (8, 80, 300, 256),
                                         # 8-bit over 256 rows: 256 x 128 blocks, K step 64; else 128 x 128, step 32
                                         (8, 300, 1000, 1024), (8, 513, 260, 192), (8, 257, 300, 64),
-                                        (8, 256, 300, 128), (8, 300, 129, 96)])
+                                        (8, 256, 300, 128), (8, 300, 129, 96),
+                                        # 4-bit split-K (33..256 rows, K >= 1024): 2, 3 and 4
+                                        # splits, a short last split, ragged N
+                                        (4, 33, 64, 4096), (4, 40, 300, 1024), (4, 100, 4100, 2048),
+                                        (4, 129, 700, 1536), (4, 256, 520, 1088), (4, 160, 2000, 1024)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
@@ -172,6 +176,27 @@ def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     Y = gpu_ctx.gemm(w, X)
     ref = oracle.gemm(X, t.payload, N, K, bits, threads=8)
     _check(Y, ref, f"gemm {M}x{N}x{K}")
+    w.free()
+
+
+def test_gemm_short_prefill_split(pe, oracle, gpu_ctx):
+    """A 128-row prefill over the config-5 weights (split K): every row
+    against the oracle, through the device entry point on a torch stream,
+    twice in a row (the second call reuses the pooled partials)."""
+    import torch
+    M, N, K = 128, 14336, 4096
+    t = pe.synth_tensor(N, K, 4, seed=pe.SEEDS["cfg5"])
+    X = pe.synth_x(M, K, seed=5)
+    w = gpu_ctx.upload_tensor(t)
+    dX = torch.from_numpy(X.view(np.int16)).cuda()
+    ref = oracle.gemm(X, t.payload, N, K, 4, threads=8)
+    s = torch.cuda.Stream()
+    for _ in range(2):
+        dY = torch.full((M, N), -1, dtype=torch.int16, device="cuda")
+        torch.cuda.synchronize()
+        gpu_ctx.gemm_dev(w, dX, M, dY, s)
+        s.synchronize()
+        _check(dY.cpu().numpy().view(np.uint16), ref, "gemm 128x14336x4096 split-K")
     w.free()
 
 
