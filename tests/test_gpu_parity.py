@@ -200,6 +200,45 @@ def test_gemm_short_prefill_split(pe, oracle, gpu_ctx):
     w.free()
 
 
+def test_graph_replay_gemv_and_split_gemm(pe, oracle, gpu_ctx):
+    """A GEMV and a split-K GEMM (its pooled partials become graph memory
+    nodes) captured in one HIP graph and replayed three times, with eager
+    library work and host synchronisation between replays: every replay
+    reproduces the eager outputs bit for bit, which match the oracle."""
+    import torch
+    M, N, K = 64, 4100, 2048
+    t = pe.synth_tensor(N, K, 4, seed=21)
+    w = gpu_ctx.upload_tensor(t)
+    X = pe.synth_x(M, K, seed=22)
+    dX = torch.from_numpy(X.view(np.int16)).cuda()
+    dYm = torch.empty((M, N), dtype=torch.int16, device="cuda")
+    dYv = torch.empty((1, N), dtype=torch.int16, device="cuda")
+    s = torch.cuda.Stream()
+    gpu_ctx.gemm_dev(w, dX, M, dYm, s)
+    gpu_ctx.gemv_dev(w, dX[:1], 1, dYv, s)
+    s.synchronize()
+    want_m = dYm.cpu().numpy().view(np.uint16).copy()
+    want_v = dYv.cpu().numpy().view(np.uint16).copy()
+    _check(want_m, oracle.gemm(X, t.payload, N, K, 4, threads=8), "eager split gemm")
+    _check(want_v, oracle.gemv(X[:1], t.payload, N, K, 4), "eager gemv")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        gpu_ctx.gemm_dev(w, dX, M, dYm, s)
+        gpu_ctx.gemv_dev(w, dX[:1], 1, dYv, s)
+    other = torch.empty((40, N), dtype=torch.int16, device="cuda")
+    for rep in range(3):
+        dYm.fill_(-1)
+        dYv.fill_(-1)
+        gpu_ctx.gemm_dev(w, dX[:40], 40, other)  # eager work on the context stream between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(dYm.cpu().numpy().view(np.uint16), want_m), f"replay {rep}: gemm differs"
+        assert np.array_equal(dYv.cpu().numpy().view(np.uint16), want_v), f"replay {rep}: gemv differs"
+    del g
+    w.free()
+
+
 def test_gemm_config5_sampled(pe, oracle, gpu_ctx):
     """Config 5 at full size (X 2048x4096, W 14336x4096 4-bit): 24 sampled
     rows against the oracle, and every row against a float32 BLAS product of
