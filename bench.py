@@ -474,8 +474,8 @@ def main() -> int:
     # 3..16, and 2 over >= 8192 rows) over >= 4096 rows run on the matrix cores
     mfma = (kind == "gemv" and N >= 4096 and K % 128 == 0 and
             (5 <= batch <= 16 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
-    # and its GEMM dispatch: 4-bit prefills of 33..256 rows split K over
-    # 128- or 256-row blocks (at most 4 splits, at least 8 K steps each)
+    # and its GEMM dispatch: prefills of up to 256 rows split K over one
+    # 128- or 256-row block (at most 4 splits, at least 8 K steps each)
     gemm4 = f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>"
     if bits == 4 and batch <= 256:
         smi = 4 if batch <= 128 else 8
@@ -485,9 +485,11 @@ def main() -> int:
             gemm4 = f"k_gemm_w4<{smi}> in {sk} K splits + k_gemm_split_sum"
     kernel_name = {"gemv": f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile",
                    "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
-                   "gemm": ("GEMV passes" if batch <= (64 if bits == 8 else 32) else
+                   "gemm": ("GEMV passes" if batch <= (48 if bits == 8 else 32) else
                             gemm4 if bits == 4 else
-                            "k_gemm8" if batch > 256 and K % 64 == 0 else "k_gemm<8>")}[kind]
+                            "k_gemm8" if batch > 256 and K % 64 == 0 else
+                            f"k_gemm8 in {min(4, 256 // -(-N // 128), (K // 64) // 8)} K splits + k_gemm_split_sum"
+                            if K % 64 == 0 and min(4, 256 // -(-N // 128), (K // 64) // 8) >= 2 else "k_gemm<8>")}[kind]
     roof["kernel"] = kernel_name
     roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb
 

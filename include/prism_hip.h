@@ -121,10 +121,10 @@ int prism_hip_gateup_swiglu_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate
 /* Y[M x dim_m] = X[M x dim_n] . W^T, fp32 accumulation, fp16 out: M
  * independent lut_gemv_cpu rows.  Replaces templates/palettized_gemm.metal
  * (never dispatched by the reference; kernel_provider.rs:233-237).
- * 4-bit prefills of 33..256 rows split K: their fp32 partials (up to
- * 4 * M * dim_m * 4 bytes) come from a stream-ordered pool the context
- * creates on first use and frees on the call's stream, so calls on
- * different streams do not share them. */
+ * Prefills of 33..256 rows (4-bit; 49..256 for 8-bit) split K: their
+ * fp32 partials (up to 4 * M * dim_m * 4 bytes) come from a stream-ordered
+ * pool the context creates on first use and frees on the call's stream,
+ * so calls on different streams do not share them. */
 int prism_hip_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t* X, uint32_t M, uint16_t* Y);
 int prism_hip_gemm_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
                        void* stream);

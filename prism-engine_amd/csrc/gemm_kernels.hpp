@@ -201,9 +201,12 @@ constexpr int GM8_BM = 256;
 constexpr int GM8_BN = 128;
 constexpr int GM8_BK = 64;
 
+// SPLIT: block (x, y) covers K steps [y kps, min(K / 64, (y + 1) kps)) and
+// writes its fp32 partial tile to part[y][M][N], as k_gemm_w4<MI, true> does.
+template <bool SPLIT>
 __global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
-                                               uint32_t N, uint32_t K) {
+                                               uint32_t N, uint32_t K, float* __restrict__ part, uint32_t kps) {
   constexpr int BM = GM8_BM, BN = GM8_BN, BK = GM8_BK, P = BK + 8;
   constexpr int XU = BM * BK / 8 / 256;  // 16-byte X chunks per thread per step (8)
   constexpr int WU = BN * BK / 16 / 256; // 16-byte index chunks per thread per step (2)
@@ -290,13 +293,14 @@ __global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, 
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
-  const uint32_t nk = K / BK;
-  gload(0);
+  const uint32_t kb = SPLIT ? blockIdx.y * kps : 0u;  // first K step
+  const uint32_t nk = SPLIT ? (K / BK - kb < kps ? K / BK - kb : kps) : K / BK;
+  gload(kb * BK);
   __syncthreads();  // sL ready
   for (uint32_t ks = 0; ks < nk; ks++) {
     lstore();
     __syncthreads();
-    if (ks + 1 < nk) gload((ks + 1) * BK);
+    if (ks + 1 < nk) gload((kb + ks + 1) * BK);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
       half8_t af[4], bf[2];
@@ -327,7 +331,12 @@ __global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, 
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const uint32_t m = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < M && n < N) Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][e]);
+        if (m < M && n < N) {
+          if constexpr (SPLIT)
+            part[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
+          else
+            Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][e]);
+        }
       }
     }
 }

@@ -326,12 +326,13 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
                 hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
-  // Up to 32 rows of X (64 for 8-bit weights): GEMV passes of up to 16
+  // Up to 32 rows of X (48 for 8-bit weights): GEMV passes of up to 16
   // vectors stream the weights M / 16 times but take less than the GEMM's
   // fixed cost.  MI355X, 14336x4096 4-bit: M = 24 / 32 / 40 / 48 take 25.7 /
   // 28.2 / 38.2 / 41.6 us as GEMVs and 31.1 / 31.5 / 31.9 / 32.8 us as the
-  // split-K GEMM; 8-bit M = 64 / 128: 85 / 171 us against 97 / 100 us.
-  if (!fast || M <= (bits == 8 ? 64u : 32u)) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
+  // split-K GEMM; 8-bit M = 32 / 48 / 64: 42.6 / 63.4 / 84.5 us against 65.2
+  // / 65.4 / 66.2 us.
+  if (!fast || M <= (bits == 8 ? 48u : 32u)) return launch_gemv(ctx, w, nullptr, d_X, M, d_Y, st);
   // 4-bit, K % 64 == 0: the MFMA kernel with register decode and LDS-DMA
   // staging (gemm_kernels.hpp, k_gemm_w4); its buffer descriptors address
   // the index block and one block's X rows with 32-bit ranges.  Blocks of
@@ -406,17 +407,53 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
   }
   // 8-bit, K % 64 == 0, more than 256 rows: 256 x 128 blocks over a 64-wide
   // K step (k_gemm8).  MI355X, 14336x4096: M = 384 / 512 / 2048 take 118 /
-  // 123 / 454 us against 197 / 206 / 701 us in k_gemm<8>'s 128 x 128 blocks,
-  // which stay ahead up to 256 rows (102 against 112 us).
-  if (bits == 8 && K % prism::GM8_BK == 0 && M > 256) {
-    const uint32_t tiles8 = ((M + prism::GM8_BM - 1) / prism::GM8_BM) * ((N + prism::GM8_BN - 1) / prism::GM8_BN);
-    const uint8_t* lut = w->lut();
-    const uint8_t* idx = w->idx();
-    const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
-    uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
-    void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K)};
-    HIP_TRY(ctx, hipLaunchKernel(reinterpret_cast<const void*>(&prism::k_gemm8), dim3(tiles8), dim3(256), args, 0, st));
-    return PRISM_HIP_OK;
+  // 123 / 454 us against 197 / 206 / 701 us in k_gemm<8>'s 128 x 128 blocks.
+  // Up to 256 rows, one M block in K splits as for 4-bit (at most 4, at
+  // least 8 K steps each; two at 14336 rows): M = 65 / 128 / 256 in 69.1 /
+  // 72.5 / 77.0 us against 95.9 / 97.8 / 102.8 in k_gemm<8>, which is left
+  // for prefills that cannot split.
+  static_assert(prism::GM8_BK == prism::GW4_BK, "one K step for both GEMMs");
+  if (bits == 8 && K % prism::GM8_BK == 0) {
+    const uint32_t nt8 = (N + prism::GM8_BN - 1) / prism::GM8_BN;
+    uint32_t sk8 = 1;
+    if (M <= 256) {
+      sk8 = (uint32_t)ctx->num_cu / nt8;
+      sk8 = sk8 < 4 ? sk8 : 4;
+      sk8 = sk8 < nsteps / 8 ? sk8 : nsteps / 8;
+    }
+    if (M > 256 || sk8 >= 2) {
+      const uint32_t tiles8 = ((M + prism::GM8_BM - 1) / prism::GM8_BM) * nt8;
+      const uint8_t* lut = w->lut();
+      const uint8_t* idx = w->idx();
+      const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
+      uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
+      const bool split = M <= 256;
+      float* P = nullptr;
+      uint32_t kps = 0, ns = 1;
+      if (split) {
+        kps = (nsteps + sk8 - 1) / sk8;
+        ns = (nsteps + kps - 1) / kps;
+        int rc = ensure_pool(ctx);
+        if (rc) return rc;
+        HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), (size_t)ns * M * N * 4, ctx->pool, st));
+      }
+      void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K), &P, &kps};
+      const void* fn = split ? reinterpret_cast<const void*>(&prism::k_gemm8<true>)
+                             : reinterpret_cast<const void*>(&prism::k_gemm8<false>);
+      hipError_t e = hipLaunchKernel(fn, dim3(tiles8, ns), dim3(256), args, 0, st);
+      if (e == hipSuccess && split) {
+        const uint64_t mn = (uint64_t)M * N;
+        hipLaunchKernelGGL(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y,
+                           mn, ns);
+        e = hipGetLastError();
+      }
+      if (split) {
+        const hipError_t f = hipFreeAsync(P, st);
+        if (e == hipSuccess) e = f;
+      }
+      if (e != hipSuccess) return fail(ctx, PRISM_HIP_ERR_DEVICE, "GEMM launch: %s", hipGetErrorString(e));
+      return PRISM_HIP_OK;
+    }
   }
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
   const uint8_t* lut = w->lut();

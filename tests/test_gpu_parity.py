@@ -168,7 +168,10 @@ def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
                                         # 4-bit split-K (33..256 rows, K >= 1024): 2, 3 and 4
                                         # splits, a short last split, ragged N
                                         (4, 33, 64, 4096), (4, 40, 300, 1024), (4, 100, 4100, 2048),
-                                        (4, 129, 700, 1536), (4, 256, 520, 1088), (4, 160, 2000, 1024)])
+                                        (4, 129, 700, 1536), (4, 256, 520, 1088), (4, 160, 2000, 1024),
+                                        # 8-bit split-K (49..256 rows, K >= 1024): 2, 3 and 4 splits
+                                        (8, 49, 300, 1024), (8, 100, 4100, 2048), (8, 256, 700, 1536),
+                                        (8, 129, 14336, 1088)])
 def test_gemm_small(pe, oracle, gpu_ctx, bits, M, N, K):
     t = pe.synth_tensor(N, K, bits, seed=M + N)
     X = pe.synth_x(M, K, seed=M)
