@@ -322,6 +322,43 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
                          w2 ? w2->idx() : nullptr, d_x, nb, d_y, st);
 }
 
+// One GEMM kernel launch over (tiles, splits) blocks, kernel signature
+// (lut, idx, X, Y, M, N, K, partials, K steps per split).  With nsplit > 1
+// the K steps are cut into splits of kps steps (every split keeps at least
+// one), the blocks write fp32 partials to a buffer from the context's
+// stream-ordered pool, and k_gemm_split_sum adds them in split order.
+int launch_gemm_blocks(prism_hip_ctx* ctx, const void* fn, uint32_t tiles, uint32_t nsteps, uint32_t nsplit,
+                       const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y, hipStream_t st) {
+  const uint8_t* lut = w->lut();
+  const uint8_t* idx = w->idx();
+  const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
+  uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
+  uint32_t N = w->dim_m, K = w->dim_n;
+  const bool split = nsplit > 1;
+  float* P = nullptr;
+  uint32_t kps = 0, ns = 1;
+  if (split) {
+    kps = (nsteps + nsplit - 1) / nsplit;
+    ns = (nsteps + kps - 1) / kps;
+    int rc = ensure_pool(ctx);
+    if (rc) return rc;
+    HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), (size_t)ns * M * N * 4, ctx->pool, st));
+  }
+  void* args[] = {&lut, &idx, &X, &Y, &M, &N, &K, &P, &kps};
+  hipError_t e = hipLaunchKernel(fn, dim3(tiles, ns), dim3(256), args, 0, st);
+  if (e == hipSuccess && split) {
+    const uint64_t mn = (uint64_t)M * N;
+    hipLaunchKernelGGL(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y, mn, ns);
+    e = hipGetLastError();
+  }
+  if (split) {
+    const hipError_t f = hipFreeAsync(P, st);
+    if (e == hipSuccess) e = f;
+  }
+  if (e != hipSuccess) return fail(ctx, PRISM_HIP_ERR_DEVICE, "GEMM launch: %s", hipGetErrorString(e));
+  return PRISM_HIP_OK;
+}
+
 int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
                 hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
@@ -366,24 +403,9 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
   const uint32_t bm = 32u * (uint32_t)mi;
   if (bits == 4 && K % prism::GW4_BK == 0 && (uint64_t)N * (K / 2) < (1ull << 31) &&
       (uint64_t)bm * K * 2 < (1ull << 31)) {
-    const uint32_t tiles4 = ((M + bm - 1) / bm) * ((N + prism::GW4_BN - 1) / prism::GW4_BN);
-    const uint8_t* lut = w->lut();
-    const uint8_t* idx = w->idx();
-    const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
-    uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
-    const bool split = nsplit > 1;
-    float* P = nullptr;
-    uint32_t kps = 0, ns = 1;
-    if (split) {
-      kps = (nsteps + nsplit - 1) / nsplit;
-      ns = (nsteps + kps - 1) / kps;  // every split has at least one K step
-      int rc = ensure_pool(ctx);
-      if (rc) return rc;
-      HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), (size_t)ns * M * N * 4, ctx->pool, st));
-    }
-    void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K), &P, &kps};
+    const uint32_t tiles4 = ((M + bm - 1) / bm) * ntn;
     const void* fn;
-    if (split)
+    if (nsplit > 1)
       fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2, true>)
            : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4, true>)
                      : reinterpret_cast<const void*>(&prism::k_gemm_w4<8, true>);
@@ -391,19 +413,7 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
       fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2, false>)
            : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4, false>)
                      : reinterpret_cast<const void*>(&prism::k_gemm_w4<8, false>);
-    hipError_t e = hipLaunchKernel(fn, dim3(tiles4, ns), dim3(256), args, 0, st);
-    if (e == hipSuccess && split) {
-      const uint64_t mn = (uint64_t)M * N;
-      hipLaunchKernelGGL(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y, mn,
-                         ns);
-      e = hipGetLastError();
-    }
-    if (split) {
-      const hipError_t f = hipFreeAsync(P, st);
-      if (e == hipSuccess) e = f;
-    }
-    if (e != hipSuccess) return fail(ctx, PRISM_HIP_ERR_DEVICE, "GEMM launch: %s", hipGetErrorString(e));
-    return PRISM_HIP_OK;
+    return launch_gemm_blocks(ctx, fn, tiles4, nsteps, nsplit, w, d_X, M, d_Y, st);
   }
   // 8-bit, K % 64 == 0, more than 256 rows: 256 x 128 blocks over a 64-wide
   // K step (k_gemm8).  MI355X, 14336x4096: M = 384 / 512 / 2048 take 118 /
@@ -423,36 +433,10 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
     }
     if (M > 256 || sk8 >= 2) {
       const uint32_t tiles8 = ((M + prism::GM8_BM - 1) / prism::GM8_BM) * nt8;
-      const uint8_t* lut = w->lut();
-      const uint8_t* idx = w->idx();
-      const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
-      uint16_t* Y = reinterpret_cast<uint16_t*>(d_Y);
-      const bool split = M <= 256;
-      float* P = nullptr;
-      uint32_t kps = 0, ns = 1;
-      if (split) {
-        kps = (nsteps + sk8 - 1) / sk8;
-        ns = (nsteps + kps - 1) / kps;
-        int rc = ensure_pool(ctx);
-        if (rc) return rc;
-        HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), (size_t)ns * M * N * 4, ctx->pool, st));
-      }
-      void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K), &P, &kps};
-      const void* fn = split ? reinterpret_cast<const void*>(&prism::k_gemm8<true>)
-                             : reinterpret_cast<const void*>(&prism::k_gemm8<false>);
-      hipError_t e = hipLaunchKernel(fn, dim3(tiles8, ns), dim3(256), args, 0, st);
-      if (e == hipSuccess && split) {
-        const uint64_t mn = (uint64_t)M * N;
-        hipLaunchKernelGGL(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y,
-                           mn, ns);
-        e = hipGetLastError();
-      }
-      if (split) {
-        const hipError_t f = hipFreeAsync(P, st);
-        if (e == hipSuccess) e = f;
-      }
-      if (e != hipSuccess) return fail(ctx, PRISM_HIP_ERR_DEVICE, "GEMM launch: %s", hipGetErrorString(e));
-      return PRISM_HIP_OK;
+      const uint32_t nsplit8 = M <= 256 ? sk8 : 1;
+      const void* fn = nsplit8 > 1 ? reinterpret_cast<const void*>(&prism::k_gemm8<true>)
+                                   : reinterpret_cast<const void*>(&prism::k_gemm8<false>);
+      return launch_gemm_blocks(ctx, fn, tiles8, nsteps, nsplit8, w, d_X, M, d_Y, st);
     }
   }
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
