@@ -203,6 +203,30 @@ def test_gemm_short_prefill_split(pe, oracle, gpu_ctx):
     w.free()
 
 
+def test_split_gemm_two_streams(pe, oracle, gpu_ctx):
+    """Two split-K GEMMs of different inputs enqueued on two streams with no
+    synchronisation between them (each gets its own pooled partials), then
+    a third on the first stream after both: every output against the oracle."""
+    import torch
+    M, N, K = 96, 2000, 2048
+    t = pe.synth_tensor(N, K, 4, seed=31)
+    w = gpu_ctx.upload_tensor(t)
+    Xs = [pe.synth_x(M, K, seed=32 + i) for i in range(3)]
+    dXs = [torch.from_numpy(X.view(np.int16)).cuda() for X in Xs]
+    dYs = [torch.full((M, N), -1, dtype=torch.int16, device="cuda") for _ in range(3)]
+    s0, s1 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    gpu_ctx.gemm_dev(w, dXs[0], M, dYs[0], s0)
+    gpu_ctx.gemm_dev(w, dXs[1], M, dYs[1], s1)
+    s0.wait_stream(s1)
+    gpu_ctx.gemm_dev(w, dXs[2], M, dYs[2], s0)
+    torch.cuda.synchronize()
+    for i in range(3):
+        _check(dYs[i].cpu().numpy().view(np.uint16), oracle.gemm(Xs[i], t.payload, N, K, 4, threads=8),
+               f"split gemm on stream, input {i}")
+    w.free()
+
+
 def test_graph_replay_gemv_and_split_gemm(pe, oracle, gpu_ctx):
     """A GEMV and a split-K GEMM (its pooled partials become graph memory
     nodes) captured in one HIP graph and replayed three times, with eager
