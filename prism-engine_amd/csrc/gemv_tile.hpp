@@ -129,7 +129,28 @@ constexpr size_t gemv_tile_lds_bytes(int threads) {
   return 4 * (tables + stage + parts + norm);
 }
 
-template <int BITS, int UPL, int R, bool DUAL, int NB, int EPI = 0>
+// LDS bytes of one wave's region when WI > 1 independent waves share a
+// workgroup (16-byte aligned: the tables are written as uint4).
+template <int BITS, int R, bool DUAL, int NB>
+constexpr size_t gemv_tile_wave_lds_bytes() {
+  return (gemv_tile_lds_bytes<BITS, R, DUAL, NB>(64) + 15) & ~(size_t)15;
+}
+
+// Orders a workgroup's LDS writes before its reads.  With WI > 1 every wave
+// works on its own rows in its own LDS region, so waiting for the wave's own
+// LDS operations is enough and the waves never wait for each other.
+template <int WI>
+__device__ __forceinline__ void tile_sync() {
+  if constexpr (WI > 1)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  else
+    __syncthreads();
+}
+
+// WI > 1: WI independent one-wave tiles per workgroup (wave v takes rows
+// (WI blockIdx.x + v) R ..), for matrices whose many small tiles would
+// otherwise cost more to dispatch than to run.
+template <int BITS, int UPL, int R, bool DUAL, int NB, int EPI = 0, int WI = 1>
 __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   static_assert(EPI == 0 || NB == 1, "norm / residual options are single-vector");
   constexpr int NM = DUAL ? 2 : 1;
@@ -137,17 +158,19 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   constexpr int IW = (BITS == 4) ? 1 : 2;    // index dwords per unit
   constexpr int LUT_DW = (BITS == 4) ? 8 : 128;  // LUT dwords per row
   static_assert(NT <= 16, "table offsets must stay within 16 KB");
-  extern __shared__ uint32_t lds[];          // dynamic LDS only: starts at address 0
+  extern __shared__ uint32_t lds_all[];      // dynamic LDS only: starts at address 0
   // LDS: [NT tables x 256 dwords][4-bit: NT*8 staged LUT dwords + T scratch |
   //       8-bit: 2T scratch][W * NT * NB partial sums][W norm partials]
 
-  const int T = blockDim.x;
+  const int T = WI > 1 ? 64 : (int)blockDim.x;
   const int W = T >> 6;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = WI > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t vw = WI > 1 ? threadIdx.x >> 6 : 0u;  // this wave's tile in the workgroup
+  uint32_t* lds = lds_all + vw * (uint32_t)(gemv_tile_wave_lds_bytes<BITS, R, DUAL, NB>() / 4);
   const uint32_t N = a.N, K = a.K;
   const uint32_t U = K / 8;
   const uint32_t row_dw = U * IW;
-  const uint32_t row0 = blockIdx.x * R;
+  const uint32_t row0 = (blockIdx.x * WI + vw) * R;
   uint32_t* stage = lds + NT * 256;
   float* part = reinterpret_cast<float*>(stage + ((BITS == 4) ? NT * 8 + T : 2 * T));
   float* nsum = part + W * NT * NB;
@@ -240,7 +263,7 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
       const int d = tid + T * i;
       stage[d < LUT_TOTAL ? d : LUT_TOTAL + tid] = lreg[i];
     }
-    __syncthreads();
+    tile_sync<WI>();
     // table t, uint4 q = entries 4q .. 4q+3 = {LUT[4(q&3) + i] | LUT[q>>2] << 16}
     const uint16_t* st16 = reinterpret_cast<const uint16_t*>(stage);
     for (int i = tid; i < NT * 64; i += T) {
@@ -261,7 +284,7 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
       *dst = make_uint2(lreg[i] & 0xFFFFu, lreg[i] >> 16);
     }
   }
-  __syncthreads();
+  tile_sync<WI>();
 
   if constexpr ((EPI & kEpiNorm) != 0) {
     // sum of squares of this thread's units (units past K read as 0)
@@ -276,7 +299,7 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
       }
     ss = wave_sum_to_lane63(ss);
     if (lane == 63) nsum[wave] = ss;
-    __syncthreads();
+    tile_sync<WI>();
     float tot = 0.0f;
     for (int w = 0; w < W; w++) tot += nsum[w];
     const float inv = 1.0f / sqrtf(tot / (float)K + a.eps);
@@ -332,7 +355,7 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
         const float v = wave_sum_to_lane63(acc[r][m][b]);
         if (lane == 63) part[((wave * R + r) * NM + m) * NB + b] = v;
       }
-  __syncthreads();
+  tile_sync<WI>();
   if (tid < R * NB) {
     const int r = tid / NB, b = tid % NB;
     const uint32_t row = row0 + r;

@@ -36,8 +36,8 @@ GEMV_SHAPES = [
     (4, 18944, 3584),    # config 2 matrix
     (4, 896, 4864),      # Qwen down_proj
     (4, 128, 896),       # Qwen k/v proj
-    (4, 151936, 896),    # Qwen tied LM head (tall: 4 rows per workgroup)
-    (4, 40001, 64),      # tall, ragged last workgroup
+    (4, 151936, 896),    # Qwen tied LM head (tall: four one-wave tiles of 4 rows per workgroup)
+    (4, 40001, 64),      # tall, ragged last workgroup (waves past the last row)
     (4, 1, 32), (4, 3, 64), (4, 17, 96), (4, 65, 160), (4, 100, 2080),
     (4, 5, 8), (4, 9, 24), (4, 7, 40), (4, 6, 100), (4, 4, 12), (4, 3, 4),  # ragged K: generic path
     (8, 14336, 4096),    # config 4
