@@ -201,10 +201,17 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
   // their bytes (measured on 151936 x 896: 47 us at R=2, 26 us at R=4), and
   // one-wave tiles go four to a workgroup (below).
   const bool tall = bits == 4 && NB == 1 && !dual && N >= 32768;
-  // waves per workgroup: the fewest that keep UPL <= uplmax; 4-bit rows of
-  // 65..128 units (K <= 1024) use 2 waves unless tall, 8-bit ones at least 4
+  // 4-bit single-vector rows of 65..128 units (K <= 1024, the decode step's
+  // and cfg1's shapes): two independent one-wave tiles per workgroup.
+  // MI355X: 4864x896 3.04 against 3.22 us with one two-wave tile (K split
+  // over the waves), the Qwen2.5-0.5B decode step 540 against 553 us/token;
+  // four tiles: 3.06 / 543.  Longer rows (cfg2's gate_up, K = 3584) lost
+  // with two or four (17.2 against 16.4 us).
+  const bool pair = bits == 4 && NB == 1 && !tall && U > 64 && U <= 128;
+  // waves per workgroup: the fewest that keep UPL <= uplmax; 8-bit rows at
+  // least 4
   uint32_t W = 0;
-  const uint32_t wmin = bits == 8 ? 4u : (U > 64 && U <= 128 && NB == 1 && !tall) ? 2u : 1u;
+  const uint32_t wmin = bits == 8 ? 4u : 1u;
   for (uint32_t w = wmin; w <= 8; w *= 2)
     if ((U + 64 * w - 1) / (64 * w) <= uplmax) {
       W = w;
@@ -214,14 +221,27 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
   const int upl = (int)((U + 64 * W - 1) / (64 * W));
   const int threads = (int)(64 * W);
   if (bits == 4) {
+    if (pair) {
+      if (dual) {
+        if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, true, 1, prism::kEpiNorm, 2>(upl, threads);
+        if (epi) return TilePlan{};
+        return tile_pick_upl<4, 2, true, 1, 0, 2>(upl, threads);
+      }
+      if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, false, 1, prism::kEpiNorm, 2>(upl, threads);
+      if (epi == prism::kEpiResid) return tile_pick_upl<4, 2, false, 1, prism::kEpiResid, 2>(upl, threads);
+      if (epi == (prism::kEpiAttnIn | prism::kEpiResid))
+        return tile_pick_upl<4, 2, false, 1, prism::kEpiAttnIn | prism::kEpiResid, 2>(upl, threads);
+      if (epi) return TilePlan{};
+      return tile_pick_upl<4, 2, false, 1, 0, 2>(upl, threads);
+    }
     if (dual) {
       if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, true, 1, prism::kEpiNorm>(upl, threads);
       if (epi) return TilePlan{};
       return tile_pick_upl<4, 2, true, 1>(upl, threads);
     }
     if (tall) {
-      // one-wave tiles, four to a workgroup: 151936 x 896 in 19.2 us against
-      // 24.7 with one tile per workgroup (38 K workgroups to dispatch)
+      // one-wave tiles, four to a workgroup: 151936 x 896 in 20.0 us against
+      // 24.8 with one tile per workgroup (38 K workgroups to dispatch)
       if (W == 1) {
         if (epi == prism::kEpiNorm) return tile_pick_upl<4, 4, false, 1, prism::kEpiNorm, 4>(upl, threads);
         if (epi == prism::kEpiResid) return tile_pick_upl<4, 4, false, 1, prism::kEpiResid, 4>(upl, threads);

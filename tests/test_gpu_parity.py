@@ -38,6 +38,7 @@ GEMV_SHAPES = [
     (4, 128, 896),       # Qwen k/v proj
     (4, 151936, 896),    # Qwen tied LM head (tall: four one-wave tiles of 4 rows per workgroup)
     (4, 40001, 64),      # tall, ragged last workgroup (waves past the last row)
+    (4, 4099, 1000), (4, 333, 520), (4, 3, 1024),  # 65..128 units: two one-wave tiles per workgroup, ragged
     (4, 1, 32), (4, 3, 64), (4, 17, 96), (4, 65, 160), (4, 100, 2080),
     (4, 5, 8), (4, 9, 24), (4, 7, 40), (4, 6, 100), (4, 4, 12), (4, 3, 4),  # ragged K: generic path
     (8, 14336, 4096),    # config 4
@@ -136,7 +137,8 @@ def test_decode_rows_bit_exact(pe, oracle, gpu_ctx, bits, N, K):
     w.free()
 
 
-@pytest.mark.parametrize("bits,N,K", [(4, 18944, 3584), (4, 4864, 896), (4, 50, 128), (4, 9, 40), (8, 700, 1024)])
+@pytest.mark.parametrize("bits,N,K", [(4, 18944, 3584), (4, 4864, 896), (4, 50, 128), (4, 9, 40), (8, 700, 1024),
+                                      (4, 333, 1000)])
 def test_gateup_swiglu(pe, oracle, gpu_ctx, bits, N, K):
     g = pe.synth_tensor(N, K, bits, seed=2 * N + 1)
     u = pe.synth_tensor(N, K, bits, seed=2 * N + 2)
