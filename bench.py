@@ -43,7 +43,7 @@ MALL_BYTES = 256 << 20
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE x 1,
 # scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_tile_hero_4bit_b1_pmc.md,
 # profiles/k_gemv_mfma_hero_4bit_b8.md, profiles/k_gemv_mfma_cfg4_8bit_b8.md
-PMC_TRAFFIC = {("hero", 1): 30641280, ("hero", 8): 31139398, ("cfg4", 8): 67160340}
+PMC_TRAFFIC = {("hero", 8): 31139398, ("cfg4", 8): 67160340}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
@@ -72,6 +72,14 @@ def cpu_model() -> str:
     except Exception:
         pass
     return platform.processor() or "unknown"
+
+
+def gi64_layout(bits: int, N: int, K: int, num_cu: int) -> bool:
+    """The library's device-layout rule (prism_hip.hip gi64_layout): 4-bit
+    matrices with K % 64 == 0, K >= 2048 and num_cu/2 .. num_cu groups of 64
+    rows are regrouped to GI64 and run on the lane-per-row GEMV."""
+    groups = -(-N // 64)
+    return bits == 4 and K % 64 == 0 and K >= 2048 and 2 * groups >= num_cu and groups <= num_cu
 
 
 def weight_bytes(bits: int, N: int, K: int) -> int:
@@ -476,15 +484,21 @@ def main() -> int:
             (5 <= batch <= 16 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
     # and its GEMM dispatch: prefills of up to 256 rows split K over one
     # 128- or 256-row block (at most 4 splits, at least 8 K steps each)
-    gemm4 = f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>"
+    gi = gi64_layout(bits, N, K, torch.cuda.get_device_properties(0).multi_processor_count)
+    gemm4 = f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" + (" (GI64)" if gi else "")
     if bits == 4 and batch <= 256:
         smi = 4 if batch <= 128 else 8
         blocks = -(-batch // (32 * smi)) * -(-N // 256)
         sk = min(4, 256 // blocks, (K // 64) // 8)
         if sk >= 2:
-            gemm4 = f"k_gemm_w4<{smi}> in {sk} K splits + k_gemm_split_sum"
-    kernel_name = {"gemv": f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile",
-                   "gateup": "k_gemv_tile (DUAL gate_up + SwiGLU)",
+            gemm4 = f"k_gemm_w4<{smi}>{' (GI64)' if gi else ''} in {sk} K splits + k_gemm_split_sum"
+    if gi:
+        gemv_name = ("k_gemv_lpr<8,1,%d> (GI64)" % batch if batch <= 2 else
+                     "k_gemv_mfma<4,GI64>" if K % 128 == 0 else "k_gemv_lpr<8,1,2> passes (GI64)")
+    else:
+        gemv_name = f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile"
+    kernel_name = {"gemv": gemv_name,
+                   "gateup": "k_gemv_lpr<16,2,1,SwiGLU> (GI64)" if gi else "k_gemv_tile (DUAL gate_up + SwiGLU)",
                    "gemm": ("GEMV passes" if batch <= (48 if bits == 8 else 32) else
                             gemm4 if bits == 4 else
                             "k_gemm8" if batch > 256 and K % 64 == 0 else

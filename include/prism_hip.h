@@ -116,6 +116,21 @@ int prism_hip_gateup_swiglu(prism_hip_ctx* ctx, const prism_hip_weight* gate, co
 int prism_hip_gateup_swiglu_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
                                 const void* d_x, void* d_y, void* stream);
 
+/* ---- gate and up GEMVs without activation (two outputs) ---------------- */
+
+/* gate_out[r] = gemv(x, gate)[r], up_out[r] = gemv(x, up)[r] (fp16 bits),
+ * in one pass over both matrices: the two raw outputs of
+ * templates/fused_gate_up.metal:16-97 (output_gate, output_up; a kernel the
+ * reference compiles but never dispatches), with the split-block layout and
+ * out_dim = dim_m.  Each output equals prism_hip_gemv of that matrix bit for
+ * bit.  For callers that apply an activation other than SiLU (for example
+ * gelu_inplace, compute-core/src/lut/evaluator.rs:86-95).  Shapes must
+ * match (ERR_MISMATCH).  x: [dim_n]; outputs: [dim_m]. */
+int prism_hip_gate_up(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
+                      const uint16_t* x, uint16_t* gate_out, uint16_t* up_out);
+int prism_hip_gate_up_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
+                          const void* d_x, void* d_gate_out, void* d_up_out, void* stream);
+
 /* ---- palettized GEMM (prefill) ------------------------------------------ */
 
 /* Y[M x dim_m] = X[M x dim_n] . W^T, fp32 accumulation, fp16 out: M

@@ -61,6 +61,8 @@ SIGNATURES = {
     "prism_hip_gemv_dev": (_c.c_int, [_vp, _vp, _vp, _c.c_uint32, _vp, _vp]),
     "prism_hip_gateup_swiglu": (_c.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "prism_hip_gateup_swiglu_dev": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "prism_hip_gate_up": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "prism_hip_gate_up_dev": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "prism_hip_gemm": (_c.c_int, [_vp, _vp, _vp, _c.c_uint32, _vp]),
     "prism_hip_gemm_dev": (_c.c_int, [_vp, _vp, _vp, _c.c_uint32, _vp, _vp]),
     "prism_hip_lut_embed": (_c.c_int, [_vp, _vp, _c.c_uint32, _vp]),

@@ -73,6 +73,17 @@ class Context:
     def upload_tensor(self, t: PalettizedTensor) -> "Weight":
         return self.upload(t.payload, t.dim_m, t.dim_n, t.bits)
 
+    def upload_dev(self, d_payload, dim_m: int, dim_n: int, bits: int) -> "Weight":
+        """Upload from a device buffer (a torch tensor or an address) holding a split-block payload."""
+        nbytes = d_payload.numel() * d_payload.element_size() if hasattr(d_payload, "numel") else None
+        if nbytes is None:
+            raise ValueError("pass a torch tensor")
+        h = self.lib.prism_hip_weight_upload_dev(self.h, ptr(d_payload), nbytes, dim_m, dim_n, bits,
+                                                 _native.LAYOUT_SPLIT_BLOCK)
+        if not h:
+            raise PrismHipError(_native.ERR_SHAPE, self.error())
+        return Weight(self, h, dim_m, dim_n, bits, nbytes)
+
     # -- host-pointer, synchronous
     def gemv(self, w: "Weight", x) -> np.ndarray:
         x = _u16(x)
@@ -88,6 +99,14 @@ class Context:
         y = np.empty(gate.dim_m, dtype=np.uint16)
         self.check(self.lib.prism_hip_gateup_swiglu(self.h, gate.h, up.h, x.ctypes.data, y.ctypes.data))
         return y
+
+    def gate_up(self, gate: "Weight", up: "Weight", x) -> tuple[np.ndarray, np.ndarray]:
+        """The raw gate and up outputs in one pass (fused_gate_up.metal's two outputs)."""
+        x = _u16(x)
+        yg = np.empty(gate.dim_m, dtype=np.uint16)
+        yu = np.empty(gate.dim_m, dtype=np.uint16)
+        self.check(self.lib.prism_hip_gate_up(self.h, gate.h, up.h, x.ctypes.data, yg.ctypes.data, yu.ctypes.data))
+        return yg, yu
 
     def gemm(self, w: "Weight", X) -> np.ndarray:
         X = _u16(X)
@@ -108,6 +127,10 @@ class Context:
     def gateup_swiglu_dev(self, gate: "Weight", up: "Weight", d_x, d_y, stream=None) -> None:
         self.check(self.lib.prism_hip_gateup_swiglu_dev(self.h, gate.h, up.h, ptr(d_x), ptr(d_y),
                                                         _stream_handle(stream)))
+
+    def gate_up_dev(self, gate: "Weight", up: "Weight", d_x, d_gate, d_up, stream=None) -> None:
+        self.check(self.lib.prism_hip_gate_up_dev(self.h, gate.h, up.h, ptr(d_x), ptr(d_gate), ptr(d_up),
+                                                  _stream_handle(stream)))
 
     def gemm_dev(self, w: "Weight", d_X, M: int, d_Y, stream=None) -> None:
         self.check(self.lib.prism_hip_gemm_dev(self.h, w.h, ptr(d_X), M, ptr(d_Y), _stream_handle(stream)))

@@ -24,6 +24,7 @@
 
 #include <type_traits>
 
+#include "gemv_lpr.hpp"
 #include "lut_perm.hpp"
 
 namespace prism {
@@ -374,11 +375,14 @@ constexpr int kGwdWord3 = 0x00020000;
 //     touches at one logical chunk then land in 16 distinct 16-byte bank
 //     groups (measured: as fast as a contiguous read, where f(r) = r & 7
 //     loses ~30 %).  One DMA instruction fills 8 rows (64 slots, lane l ->
-//     slot l): lane l loads row 8i + l/8, chunk (l%8) ^ (l/8) ^ (i & 1), a
-//     per-lane byte offset (two, by the parity of i) fixed for the whole
-//     loop, the row block and K step going into the scalar offset;
+//     slot l): lane l loads row 8i + l/8, chunk (l%8) ^ (l/8) ^ (i & 1).
+//     The row goes in the per-lane VGPR offset, which the descriptor's
+//     range check covers, and only the K step in the scalar offset, which
+//     it does not: a row past M then reads as 0 without touching memory,
+//     and a row inside it stays inside it at every K step;
 //   - index part: 256 weight rows x 32 bytes (this K step's 64 nibbles),
-//     2 slots per row; wave w fills its own 64 rows with 2 instructions.
+//     2 slots per row; wave w fills its own 64 rows with 2 instructions,
+//     the row again in the VGPR offset and the K step in the scalar one.
 // * Schedule of K step it (stage it % 3): MFMA steps 0..2 each read the next
 //   step's A fragments and decode its B operands (double buffers) under
 //   their own 16 MFMAs.  Before MFMA step 3 the wave waits for its reads of
@@ -393,7 +397,8 @@ constexpr int kGwdWord3 = 0x00020000;
 //   W tiles and X rows one XCD works on stay in its own L2.
 // Requires K % 64 == 0, 16-byte aligned X, an index block below 2 GiB and
 // 256 * K * 2 bytes of X per block below 2 GiB (the buffer descriptors'
-// 32-bit ranges; rows past M or N read as 0 through the range check).
+// 32-bit ranges; rows past M or N read as 0 through the range check of the
+// VGPR offset).
 constexpr int GWD_STAGES = 3;
 constexpr int GWD_WSLOTS = GW4_BN * 2;  // 16-byte index slots per stage
 
@@ -420,10 +425,14 @@ __device__ __forceinline__ void gwd_wait_vm() {
 
 // MI = 32-row M subtiles per block (BM = 32 MI): 8 for long prefills; 2 and
 // 4 give short ones (65..1024 rows) more blocks.
+// GI: the weights are in the GI64 layout (gemv_lpr.hpp; lut and idx both
+// point at it).  Wave w's 64 rows are one GI64 group, so a K step's index
+// bytes are two contiguous 1 KB chunks (one DMA instruction each, lane l ->
+// row l) and slot (c, r) of the index part holds chunk c of row r.
 // SPLIT: block (x, y) covers K steps [y kps, min(K / 64, (y + 1) kps)) and
 // writes its fp32 partial tile to P[y][M][N] (k_gemm_split_sum adds the
 // partials); otherwise the whole K range, fp16 to Y.
-template <int MI, bool SPLIT>
+template <int MI, bool SPLIT, bool GI = false>
 __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                  const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
                                                  uint32_t N, uint32_t K, float* __restrict__ P, uint32_t kps) {
@@ -462,28 +471,35 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   for (int s = 0; s < 2; s++) {
     uint32_t n = n0 + 64 * wave + 32 * s + j;
     n = n < N ? n : N - 1;
-    const uint4* lr = reinterpret_cast<const uint4*>(lut + (size_t)n * 32);
+    const uint4* lr = reinterpret_cast<const uint4*>(lut + (GI ? gi64_lut_offset(n, K) : (size_t)n * 32));
     pl[s] = make_planes(lr[0], lr[1]);
   }
   // ---- DMA sources; reads past the descriptors' ranges return 0
   const uint32_t live = (M - m0 < (uint32_t)BM) ? M - m0 : (uint32_t)BM;
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(X + (size_t)m0 * K), (short)0, (int)(live * K * 2u), kGwdWord3);
-  const __amdgpu_buffer_rsrc_t rw =
-      __builtin_amdgcn_make_buffer_rsrc((void*)idx, (short)0, (int)(N * row_bytes), kGwdWord3);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)idx, (short)0, (int)(GI ? (uint32_t)gi64_bytes(N, K) : N * row_bytes), kGwdWord3);
   const uint32_t lr8 = (uint32_t)lane >> 3, lc = ((uint32_t)lane & 7u) ^ lr8;
+  // Per-lane VGPR offsets of each DMA instruction (row and chunk); the
+  // scalar offset carries only the K step.
   const uint32_t xv0 = ((uint32_t)XR * wave + lr8) * K * 2u + 16u * lc;  // even DMA index
-  const uint32_t xv1 = xv0 ^ 16u;                                // odd: chunk lc ^ 1
-  const uint32_t wv = (n0 + 64u * wave + ((uint32_t)lane >> 1)) * row_bytes + 16u * ((uint32_t)lane & 1u);
+  uint32_t xv[MI];
+#pragma unroll
+  for (int i = 0; i < MI; i++) xv[i] = ((i & 1) ? (xv0 ^ 16u) : xv0) + (uint32_t)i * 16u * K;  // odd: chunk lc ^ 1
+  // GI64: instruction i reads chunk 2 (it + kb) + i of the wave's group (the
+  // group base is past the range for groups past N: zeros)
+  const uint32_t wv0 = GI ? (uint32_t)((size_t)((n0 + 64u * wave) / kGiRows) * gi64_group_bytes(K)) + kGiLutBytes +
+                                (uint32_t)lane * 16u
+                          : (n0 + 64u * wave + ((uint32_t)lane >> 1)) * row_bytes + 16u * ((uint32_t)lane & 1u);
+  const uint32_t wv[2] = {wv0, GI ? wv0 + 1024u : wv0 + 32u * row_bytes};
 
   auto issue = [&](uint32_t it, int stage) {
     uint4* st = sx + stage * SL;
 #pragma unroll
-    for (int i = 0; i < MI; i++)
-      gwd_dma16(rx, st + 64 * (MI * wave + i), (i & 1) ? xv1 : xv0, (uint32_t)i * 16u * K + (it + kb) * 128u);
+    for (int i = 0; i < MI; i++) gwd_dma16(rx, st + 64 * (MI * wave + i), xv[i], (it + kb) * 128u);
 #pragma unroll
-    for (int i = 0; i < 2; i++)
-      gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv, (uint32_t)i * 32u * row_bytes + (it + kb) * 32u);
+    for (int i = 0; i < 2; i++) gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv[i], (it + kb) * (GI ? 2048u : 32u));
   };
   auto wdword = [](const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; };
 
@@ -500,14 +516,15 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   // 2 * (64 wave + 32 s + j) + h of the index part.
   const uint32_t arow = (uint32_t)j * 8u;
   const uint32_t asw = ((uint32_t)j & 7u) ^ (((uint32_t)j >> 3) & 1u);
-  const uint32_t wsl = 2u * (64u * wave + j) + h;
+  const uint32_t wsl = GI ? 128u * wave + 64u * h + j : 2u * (64u * wave + j) + h;
+  constexpr uint32_t WS1 = GI ? 32u : 64u;  // slot step from row j to row 32 + j
 
   half8_t a[2][MI];
   half8_t bop[2][2];
   uint4 wch[2];
   auto read_first = [&](const uint4* st) {  // index chunks + MFMA step 0's A fragments
     wch[0] = st[XS + wsl];
-    wch[1] = st[XS + wsl + 64];
+    wch[1] = st[XS + wsl + WS1];
 #pragma unroll
     for (int i = 0; i < MI; i++) a[0][i] = __builtin_bit_cast(half8_t, st[256 * i + arow + ((4u * h) ^ asw)]);
   };
@@ -570,7 +587,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     const uint4* sn = sx + SNX * SL;
     if (more) {
       wch[0] = sn[XS + wsl];
-      wch[1] = sn[XS + wsl + 64];
+      wch[1] = sn[XS + wsl + WS1];
     }
 #pragma unroll
     for (int i = 0; i < MI; i++) {

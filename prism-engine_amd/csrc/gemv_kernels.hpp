@@ -52,6 +52,7 @@ struct GemvArgs {
   const uint8_t* idx2;
   const uint16_t* x;    // [nb][K] fp16
   uint16_t* y;          // [nb][N] fp16
+  uint16_t* y2;         // DUAL with the pair epilogue: the up output [N]
   uint32_t N;
   uint32_t K;
   uint32_t nb;          // live batch rows (<= NB)
@@ -63,8 +64,39 @@ struct GemvArgs {
 // unaligned x): one wave per row, element-strided.  Follows lut_gemv_cpu's
 // ragged-K rule for 4-bit weights: row stride K/2 bytes, only the first
 // (K/8)*8 elements contribute.
-template <int BITS, bool DUAL>
+// GI64: the group-interleaved 4-bit device layout (k_gemv_lpr, gemv_lpr.hpp,
+// describes it): ceil(N/64) groups of [64 x 32 B LUTs][K/32 chunks][64
+// rows][16 B], rows past N zero.
+constexpr int kGiRows = 64;                // rows per group
+constexpr int kGiChunk = 16;               // index bytes per chunk (32 elements)
+constexpr int kGiLutBytes = kGiRows * 32;  // LUT block at the start of a group
+
+__host__ __device__ __forceinline__ size_t gi64_group_bytes(uint32_t K) {
+  return (size_t)kGiLutBytes + (size_t)kGiRows * (K / 2);
+}
+__host__ __device__ __forceinline__ size_t gi64_bytes(uint32_t N, uint32_t K) {
+  return (size_t)((N + kGiRows - 1) / kGiRows) * gi64_group_bytes(K);
+}
+// Byte offset of row r's LUT, of its chunk c, and of the byte holding its
+// element k.
+__host__ __device__ __forceinline__ size_t gi64_lut_offset(uint32_t r, uint32_t K) {
+  return (size_t)(r / kGiRows) * gi64_group_bytes(K) + (size_t)(r % kGiRows) * 32;
+}
+__host__ __device__ __forceinline__ size_t gi64_chunk_offset(uint32_t r, uint32_t c, uint32_t K) {
+  return (size_t)(r / kGiRows) * gi64_group_bytes(K) + kGiLutBytes +
+         ((size_t)c * kGiRows + (r % kGiRows)) * kGiChunk;
+}
+__host__ __device__ __forceinline__ size_t gi64_index_at(uint32_t r, uint32_t k, uint32_t K) {
+  return gi64_chunk_offset(r, k / 32, K) + (k % 32) / 2;
+}
+
+// MODE: kGenSingle, or gate + up rows (lut2/idx2) with the SwiGLU
+// epilogue (kGenSwiglu) or the two raw outputs y, y2 (kGenPair).
+// GI: 4-bit weights in the GI64 layout (a.lut and a.idx both point at it).
+constexpr int kGenSingle = 0, kGenSwiglu = 1, kGenPair = 2;
+template <int BITS, int MODE, bool GI = false>
 __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
+  constexpr bool DUAL = MODE != kGenSingle;
   const uint32_t row = blockIdx.x;
   const int lane = threadIdx.x;
   const uint32_t K = a.K, N = a.N;
@@ -75,13 +107,13 @@ __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
   for (uint32_t b = 0; b < nb; b++) {
     float acc[NM];
     for (int m = 0; m < NM; m++) {
-      const uint8_t* lut = (m == 0 ? a.lut : a.lut2) + (size_t)row * (2u << BITS);
-      const uint8_t* idx = (m == 0 ? a.idx : a.idx2) + (size_t)row * stride;
+      const uint8_t* lut = (m == 0 ? a.lut : a.lut2) + (GI ? gi64_lut_offset(row, K) : (size_t)row * (2u << BITS));
+      const uint8_t* idx = (m == 0 ? a.idx : a.idx2) + (GI ? 0 : (size_t)row * stride);
       float s = 0.0f;
       for (uint32_t k = lane; k < keff; k += 64) {
         uint32_t e;
         if (BITS == 4) {
-          const uint8_t byte = idx[k >> 1];
+          const uint8_t byte = GI ? idx[gi64_index_at(row, k, K)] : idx[k >> 1];
           e = (k & 1) ? (byte >> 4) : (byte & 15u);
         } else {
           e = idx[k];
@@ -92,10 +124,14 @@ __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
       acc[m] = group_sum<64>(s);
     }
     if (lane == 0) {
-      if (DUAL)
+      if constexpr (MODE == kGenSwiglu) {
         a.y[row] = swiglu_h(acc[0], acc[NM - 1]);
-      else
+      } else if constexpr (MODE == kGenPair) {
+        a.y[row] = f2h(acc[0]);
+        a.y2[row] = f2h(acc[NM - 1]);
+      } else {
         a.y[(size_t)b * N + row] = f2h(acc[0]);
+      }
     }
   }
 }
@@ -104,7 +140,8 @@ __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
 // (the per-row form of lut_embed, compute-core/src/lut/evaluator.rs:176-197).
 // For 4-bit weights elements at k >= (K/8)*8 are written as 0, matching
 // lut_embed's shorter output zero-padded.
-template <int BITS>
+// GI: 4-bit weights in the GI64 layout (lut and idx both point at it).
+template <int BITS, bool GI = false>
 __global__ __launch_bounds__(256) void k_decode_rows(const uint8_t* lut, const uint8_t* idx, uint32_t N,
                                                      uint32_t K, uint32_t row0, uint32_t nrows, uint16_t* out) {
   const uint32_t stride = (BITS == 4) ? K / 2 : K;
@@ -118,12 +155,12 @@ __global__ __launch_bounds__(256) void k_decode_rows(const uint8_t* lut, const u
     if (r < N && k < keff) {
       uint32_t e;
       if (BITS == 4) {
-        const uint8_t byte = idx[(size_t)r * stride + (k >> 1)];
+        const uint8_t byte = GI ? idx[gi64_index_at(r, k, K)] : idx[(size_t)r * stride + (k >> 1)];
         e = (k & 1) ? (byte >> 4) : (byte & 15u);
       } else {
         e = idx[(size_t)r * stride + k];
       }
-      const uint8_t* l = lut + (size_t)r * (2u << BITS) + 2 * e;
+      const uint8_t* l = lut + (GI ? gi64_lut_offset(r, K) : (size_t)r * (2u << BITS)) + 2 * e;
       v = (uint16_t)(l[0] | (l[1] << 8));
     }
     out[t] = v;

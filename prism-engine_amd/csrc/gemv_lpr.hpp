@@ -1,0 +1,274 @@
+// gemv_lpr.hpp -- lane-per-row palettized GEMV for gfx950 over the
+// group-interleaved 4-bit device layout (GI64), and the layout itself.
+//
+// y[b, r] = f16( sum_k f32(x[b, k]) * f32(LUT_r[idx(r, k)]) ): the
+// arithmetic of lut_gemv_cpu (compute-core/src/lut/evaluator.rs:21-44),
+// fp32 accumulation, fp16 output (RNE).  NM = 2 runs a gate and an up
+// matrix of the same shape over the same x: either the SwiGLU epilogue of
+// the CPU path (evaluator.rs:78-83,209-225, engine_impl.rs:1349-1374) or the
+// two raw outputs of fused_gate_up.metal (templates/fused_gate_up.metal:16-97).
+//
+// GI64 device layout (written at upload by k_gi64_pack, 4-bit, K % 64 == 0):
+//   ceil(N/64) row groups of gi64_group_bytes(K) bytes each:
+//     [64 x 32 B fp16 LUTs of the group's rows][K/32 chunks][64 rows][16 B]
+//   chunk c of row r holds index bytes 16c .. 16c+15 of the split-block row
+//   (elements 32c .. 32c+31, element 2i = low nibble of byte i).  Rows past
+//   N in the last group are zero.  A wave's 16-byte-per-lane load reads
+//   chunk c of 64 consecutive rows: 1 KB contiguous.  A group's LUTs sit
+//   right before its chunks, so they come from the same DRAM pages as the
+//   first chunks (in a separate block the LUT requests returned late, behind
+//   the index stream).  Bytes are the split-block payload's, rearranged
+//   (plus the zero rows of the last group).
+//
+// Work layout: one workgroup of S waves per group.  Lane l owns row
+// 64 g + l for the whole kernel; wave w owns a contiguous range of the
+// row's chunks (the S ranges partition K/32), so every lane of a wave
+// reads the same x elements at the same time and x lives in SGPRs
+// (scalar loads; v_dot2 takes it as its scalar operand).
+//  * Lookup tables are bank-private: the 256-entry pair table of the row
+//    of lane l (entry b = LUT[b & 15] | LUT[b >> 4] << 16, the fp16 pair of
+//    an index byte) sits at LDS dword 64 b + l, so lane l only ever reads
+//    bank l and no lookup conflicts (a table shared by the wave loses about
+//    half its LDS cycles to conflicts).  One v_perm builds the address
+//    (lane*4 in byte 0, the index byte in byte 1) and one ds_read_b32 reads
+//    the pair: per element one VALU op and half an LDS read, plus the v_dot2.
+//  * Loads: the LUTs, the first P chunks per wave and the first x block go
+//    out first; after the table build each wave keeps P chunk loads in
+//    flight, so the index stream is requested at the rate the lookups
+//    consume it (with every chunk requested up front, the waves whose
+//    chunks return last decode all of theirs at the end).  Chunk loads are
+//    unconditional (past the wave's range they read zeros through the range
+//    check), so the compiler's wait counts stay exact instead of falling
+//    back to waiting for every load.
+//  * The S wave partials of each row are added in LDS in wave order and
+//    rounded once.
+// Requires K % 64 == 0, 64-byte aligned x rows (scalar loads of 16 dwords)
+// and the weight block below 2 GiB (32-bit buffer offsets; each offset, row
+// and chunk included, is the per-lane VGPR offset, which the range check
+// covers).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemv_kernels.hpp"
+#include "gemv_tile.hpp"
+
+namespace prism {
+
+constexpr int kLprTableDw = 256 * kGiRows;  // dwords of one group's pair tables (64 KB)
+
+// Epilogues of k_gemv_lpr.
+constexpr int kLprPlain = 0;   // y[b][row] = f16(acc)
+constexpr int kLprSwiglu = 1;  // NM = 2: y[row] = swiglu(f16(gate), f16(up))
+constexpr int kLprPair = 2;    // NM = 2: y[row] = f16(gate), y2[row] = f16(up)
+
+struct LprArgs {
+  const uint8_t* w;    // GI64 weights
+  const uint8_t* w2;   // NM = 2: up matrix, same shape
+  const uint16_t* x;   // [nb][K] fp16
+  uint16_t* y;         // [nb][N]
+  uint16_t* y2;        // kLprPair: up output [N]
+  uint32_t N;
+  uint32_t K;
+  uint32_t nb;         // live batch vectors (<= NB)
+};
+
+template <int S, int NM, int NB, int EPI>
+__global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
+  static_assert(S == 4 || S == 8 || S == 16, "waves per group");
+  static_assert(NM == 1 || NM == 2, "one matrix or gate + up");
+  static_assert(NB == 1 || NB == 2, "batch vectors per pass");
+  static_assert(EPI == kLprPlain || (NM == 2 && NB == 1), "gate/up epilogues are single-vector");
+  // x chunks per scalar block (16 SGPRs per chunk and vector) and chunk
+  // loads in flight per wave (a ring of P slots, refilled in order)
+  constexpr int XB = (NM == 1 && NB == 1) ? 4 : 2;
+  constexpr int P = XB;
+  constexpr int LO = 16 / S;  // low nibbles of the table entries a thread builds
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+  // static LDS: the tables' address is a link-time constant, so a lookup
+  // needs no per-read add
+  __shared__ uint32_t lds[NM * kLprTableDw + S * NM * NB * 64];
+  float* red = reinterpret_cast<float*>(lds + NM * kLprTableDw);
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t g = blockIdx.x;
+  const uint32_t N = a.N, K = a.K, NC = K / 32;
+  const uint32_t row = g * kGiRows + lane;
+  const uint32_t c0 = (w * NC) / S, nch = ((w + 1) * NC) / S - c0;
+  const uint32_t gbase = g * (uint32_t)gi64_group_bytes(K);
+
+  // ---- the LUTs of the lane's row: 8 dwords and its LO low-nibble entries
+  // (entry e = w + S i: low nibble w + S (i % LO), high nibble i / LO).
+  // Lanes past N read the zero LUT slots of the last group's padding rows.
+  uint32_t L[NM][8], hv[NM][LO];
+#pragma unroll
+  for (int m = 0; m < NM; m++) {
+    const uint8_t* lb = (m == 0 ? a.w : a.w2) + gbase + lane * 32u;
+    const uint4 l0 = reinterpret_cast<const uint4*>(lb)[0], l1 = reinterpret_cast<const uint4*>(lb)[1];
+    L[m][0] = l0.x; L[m][1] = l0.y; L[m][2] = l0.z; L[m][3] = l0.w;
+    L[m][4] = l1.x; L[m][5] = l1.y; L[m][6] = l1.z; L[m][7] = l1.w;
+#pragma unroll
+    for (int j = 0; j < LO; j++) hv[m][j] = reinterpret_cast<const uint16_t*>(lb)[w + S * j];
+  }
+
+  // ---- index chunks: a ring of P per matrix.  Every load is issued
+  // unconditionally, so the wait counts are static; a chunk past the wave's
+  // range gets an offset past the buffer's range, which the range check
+  // turns into zeros without a memory access.
+  __amdgpu_buffer_rsrc_t ri[NM];
+  const uint32_t nbytes = ((N + kGiRows - 1) / kGiRows) * (uint32_t)gi64_group_bytes(K);
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+    ri[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(m == 0 ? a.w : a.w2), (short)0, (int)nbytes, kBufferWord3);
+  const uint32_t vbase = gbase + kGiLutBytes + (c0 * kGiRows + lane) * kGiChunk;
+  u32x4v ring[P][NM];
+  auto ldc = [&](uint32_t i, u32x4v (&dst)[NM]) {
+    const uint32_t vo = i < nch ? vbase + i * (kGiRows * kGiChunk) : 0x80000000u;
+#pragma unroll
+    for (int m = 0; m < NM; m++) dst[m] = __builtin_amdgcn_raw_buffer_load_b128(ri[m], vo, 0u, kNontemporal);
+  };
+#pragma unroll
+  for (int u = 0; u < P; u++) ldc(u, ring[u]);
+
+  // ---- first x block (scalar loads; x rows are read past the wave's range
+  // only inside the row, so no guard is needed for them)
+  const u32x16* xw[NB];
+#pragma unroll
+  for (int b = 0; b < NB; b++) {
+    const uint32_t bb = (uint32_t)b < a.nb ? (uint32_t)b : 0u;
+    xw[b] = reinterpret_cast<const u32x16*>(a.x + (size_t)bb * K) + c0;
+  }
+  u32x16 xs[NB][XB];
+  auto ldx = [&](uint32_t i) {
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int u = 0; u < XB; u++) xs[b][u] = xw[b][i + u < nch ? i + u : 0];
+  };
+  ldx(0);
+
+  // ---- bank-private pair tables
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int i = 0; i < 256 / S; i++) {
+      const int hi = i / LO;
+      const uint32_t v = __builtin_amdgcn_perm(L[m][hi >> 1], hv[m][i % LO], (hi & 1) ? 0x07060100u : 0x05040100u);
+      lds[m * kLprTableDw + (w + S * i) * 64 + lane] = v;
+    }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- lookups and products.  Chunk i + u uses ring slot u and x block
+  // entry u; its slot is refilled with chunk i + u + P once its table
+  // addresses are formed.  Full blocks of XB chunks run without branches;
+  // the last partial block skips its missing chunks.
+  const uint32_t lanebase = lane * 4u;
+  float acc[NM][NB][2];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[m][b][0] = acc[m][b][1] = 0.0f;
+  auto chunk = [&](uint32_t c, int u) {
+    uint32_t pr[NM][16];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const uint32_t ad = __builtin_amdgcn_perm(ring[u][m][j >> 2], lanebase, 0x0C0C0000u | ((4u + (j & 3)) << 8));
+        pr[m][j] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds + m * kLprTableDw) + ad);
+      }
+    ldc(c + P, ring[u]);
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[m][b][j & 1] = dot2(pr[m][j], xs[b][u][j], acc[m][b][j & 1]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const uint32_t nfull = nch / XB;
+  uint32_t i = 0;
+  for (uint32_t it = 0; it < nfull; it++, i += XB) {
+    if (it != 0) ldx(i);
+#pragma unroll
+    for (int u = 0; u < XB; u++) chunk(i + u, u);
+  }
+  if (i < nch) {
+    if (i != 0) ldx(i);
+#pragma unroll
+    for (int u = 0; u < XB - 1; u++)
+      if (i + u < nch) chunk(i + u, u);
+  }
+
+  // ---- wave partials -> LDS -> rows (waves 0 .. NB-1 finish one vector each)
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) red[((w * NM + m) * NB + b) * 64 + lane] = acc[m][b][0] + acc[m][b][1];
+  __syncthreads();
+  if (w < (uint32_t)NB) {
+    const uint32_t b = w;
+    float s[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+      s[m] = 0.0f;
+#pragma unroll
+      for (int v = 0; v < S; v++) s[m] += red[((v * NM + m) * NB + b) * 64 + lane];
+    }
+    if (row < N && b < a.nb) {
+      if constexpr (EPI == kLprSwiglu)
+        a.y[row] = swiglu_h(s[0], s[1]);
+      else if constexpr (EPI == kLprPair) {
+        a.y[row] = f2h(s[0]);
+        a.y2[row] = f2h(s[1]);
+      } else
+        a.y[(size_t)b * N + row] = f2h(s[0]);
+    }
+  }
+}
+
+// Split-block payload (LUT block then index rows) -> GI64.  One thread per
+// 16-byte piece of the GI64 block, in GI64 order: the writes are contiguous,
+// the reads 16 bytes each.  Rows past N get zero LUTs and zero indices.
+__global__ __launch_bounds__(256) void k_gi64_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                   uint32_t N, uint32_t K) {
+  const uint32_t NC = K / 32;
+  const uint32_t per_group = kGiLutBytes / 16 + NC * kGiRows;  // 16-byte pieces per group
+  const size_t total = (size_t)((N + kGiRows - 1) / kGiRows) * per_group;
+  const uint8_t* sidx = src + (size_t)N * 32;
+  for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t g = (uint32_t)(t / per_group), p = (uint32_t)(t % per_group);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (p < kGiLutBytes / 16) {  // LUT piece: row p/2, half p%2
+      const uint32_t r = g * kGiRows + p / 2;
+      if (r < N) v = *reinterpret_cast<const uint4*>(src + (size_t)r * 32 + (p % 2) * 16);
+    } else {
+      const uint32_t q = p - kGiLutBytes / 16, c = q / kGiRows, r = g * kGiRows + q % kGiRows;
+      if (r < N) v = *reinterpret_cast<const uint4*>(sidx + (size_t)r * (K / 2) + (size_t)c * kGiChunk);
+    }
+    *reinterpret_cast<uint4*>(dst + t * 16) = v;
+  }
+}
+
+// GI64 -> split-block rows: LUTs to dst_lut ([N][32] B), index rows to
+// dst_idx ([N][K/2] B), for consumers that keep split-block rows (the
+// decode-step model's own weight copies).
+__global__ __launch_bounds__(256) void k_gi64_unpack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst_lut,
+                                                     uint8_t* __restrict__ dst_idx, uint32_t N, uint32_t K) {
+  const uint32_t NC = K / 32;
+  const size_t pieces = (size_t)N * (2 + NC);  // per row: 2 LUT pieces + NC chunks
+  for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < pieces; t += (size_t)gridDim.x * blockDim.x) {
+    const uint32_t r = (uint32_t)(t / (2 + NC)), p = (uint32_t)(t % (2 + NC));
+    if (p < 2)
+      *reinterpret_cast<uint4*>(dst_lut + (size_t)r * 32 + p * 16) =
+          *reinterpret_cast<const uint4*>(src + gi64_lut_offset(r, K) + p * 16);
+    else
+      *reinterpret_cast<uint4*>(dst_idx + (size_t)r * (K / 2) + (size_t)(p - 2) * kGiChunk) =
+          *reinterpret_cast<const uint4*>(src + gi64_chunk_offset(r, p - 2, K));
+  }
+}
+
+}  // namespace prism

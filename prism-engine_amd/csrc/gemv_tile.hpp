@@ -17,8 +17,11 @@
 //  * the LUT dwords, the x units and every index unit of the R rows are
 //    issued up front (straight-line code), so the compiler counts them with
 //    vmcnt and each row is decoded as soon as its bytes land; x and index
-//    loads are buffer loads (one lane offset, the unit step as an
-//    immediate, range checking instead of clamping arithmetic);
+//    loads are buffer loads whose whole offset (row, unit) is the per-lane
+//    VGPR offset: the descriptor's range check covers the VGPR and
+//    immediate offsets only, never the scalar one, so a unit past the end
+//    of x or of the index block reads as 0 only because its offset is
+//    there;
 //  * lookup tables live in LDS at fixed addresses (table t at byte t*1024),
 //    built once per workgroup:
 //      4-bit: pair table, entry b = LUT[b & 15] | LUT[b >> 4] << 16, so one
@@ -93,9 +96,14 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
 //            [kAttnSplits][2 + 64] fp32): each thread combines its own units
 //            (head u/8, dims 8*(u%8)..+7) and rounds them to fp16, the value
 //            k_step_attn_combine would store.
+//  kEpiPair  DUAL only: instead of the SwiGLU epilogue, the raw gate and up
+//            outputs y[row] = f16(gate), y2[row] = f16(up) (the outputs of
+//            templates/fused_gate_up.metal:16-97; the CPU path computes them
+//            as two lut_gemv_cpu calls).
 constexpr int kEpiNorm = 1;
 constexpr int kEpiResid = 2;
 constexpr int kEpiAttnIn = 4;
+constexpr int kEpiPair = 8;
 
 // Buffer descriptor word 3 for gfx9-family (CDNA) raw buffers: 32-bit
 // data format, no swizzle; the range check is against num_records bytes.
@@ -103,12 +111,13 @@ constexpr int kBufferWord3 = 0x00020000;
 // Cache-policy operand of the buffer-load builtins: nontemporal.
 constexpr int kNontemporal = 2;
 // Index loads stream (nontemporal) except in the decode step's per-layer
-// projections (EPI set, 2 rows per workgroup): those weights are re-read
-// every token, and keeping them cacheable measured 1792 against 1745
-// tokens/s on the Qwen2.5-0.5B step (its LM head, R = 4, still streams).
+// projections (norm / residual / attention-input options, 2 rows per
+// workgroup): those weights are re-read every token, and keeping them
+// cacheable measured 1792 against 1745 tokens/s on the Qwen2.5-0.5B step
+// (its LM head, R = 4, still streams).
 template <int EPI, int R>
 constexpr int tile_index_aux() {
-  return (EPI != 0 && R == 2) ? 0 : kNontemporal;
+  return ((EPI & ~kEpiPair) != 0 && R == 2) ? 0 : kNontemporal;
 }
 
 // Minimum threads per workgroup by index width: the 8-bit LUT loads are
@@ -153,6 +162,7 @@ __device__ __forceinline__ void tile_sync() {
 template <int BITS, int UPL, int R, bool DUAL, int NB, int EPI = 0, int WI = 1>
 __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   static_assert(EPI == 0 || NB == 1, "norm / residual options are single-vector");
+  static_assert((EPI & kEpiPair) == 0 || DUAL, "the pair epilogue is gate + up");
   constexpr int NM = DUAL ? 2 : 1;
   constexpr int NT = NM * R;                 // lookup tables (matrix-major)
   constexpr int IW = (BITS == 4) ? 1 : 2;    // index dwords per unit
@@ -190,11 +200,13 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
     lreg[i] = lb[(size_t)rc * LUT_DW + dd % LUT_DW];
   }
 
-  // ---- x units and the index units of the R rows, as buffer loads: one
-  // lane offset, the unit step as an immediate/scalar offset, and the
-  // descriptor's range check in place of address clamping (a unit past the
-  // end of x or of the index block reads as 0; lanes past the row's last
-  // unit never use theirs).  Index loads: tile_index_aux.
+  // ---- x units and the index units of the R rows, as buffer loads.  The
+  // row and unit offsets go in the VGPR offset (the compiler moves constant
+  // parts to the immediate field), which the descriptor's range check
+  // covers; the scalar offset, which it does not cover, stays 0.  So a unit
+  // past the end of x or of the index block reads as 0 and touches no
+  // memory; lanes past the row's last unit never use theirs.  Index loads:
+  // tile_index_aux.
   typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
   typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
   uint32_t xr[NB][UPL][4];
@@ -219,7 +231,7 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
         __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + (size_t)bb * K), (short)0, (int)(K * 2), kBufferWord3);
 #pragma unroll
     for (int t = 0; t < UPL; t++) {
-      const u32x4v_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)tid * 16u, (uint32_t)(16 * T * t), 0);
+      const u32x4v_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)(tid + T * t) * 16u, 0u, 0);
       xr[b][t][0] = v.x;
       xr[b][t][1] = v.y;
       xr[b][t][2] = v.z;
@@ -241,12 +253,11 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
     for (int m = 0; m < NM; m++) {
 #pragma unroll
       for (int t = 0; t < UPL; t++) {
-        const uint32_t so = rc * row_dw * 4u + (uint32_t)(4 * IW * T * t);
+        const uint32_t vo = rc * row_dw * 4u + (uint32_t)(tid + T * t) * (4u * IW);
         if constexpr (IW == 1) {
-          iv[r][m][t][0] =
-              __builtin_amdgcn_raw_buffer_load_b32(ri[m], (uint32_t)tid * 4u, so, tile_index_aux<EPI, R>());
+          iv[r][m][t][0] = __builtin_amdgcn_raw_buffer_load_b32(ri[m], vo, 0u, tile_index_aux<EPI, R>());
         } else {
-          const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(ri[m], (uint32_t)tid * 8u, so, kNontemporal);
+          const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(ri[m], vo, 0u, kNontemporal);
           iv[r][m][t][0] = v.x;
           iv[r][m][t][1] = v.y;
         }
@@ -286,13 +297,16 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
   }
   tile_sync<WI>();
 
+  const bool last_live = (uint32_t)(tid + T * (UPL - 1)) < U;
   if constexpr ((EPI & kEpiNorm) != 0) {
-    // sum of squares of this thread's units (units past K read as 0)
+    // sum of squares of this thread's units; a unit past K is skipped (its
+    // load already read 0 through the range check)
     float ss = 0.0f;
 #pragma unroll
     for (int t = 0; t < UPL; t++)
 #pragma unroll
       for (int e = 0; e < 4; e++) {
+        if (t == UPL - 1 && !last_live) continue;
         const float lo = h2f((uint16_t)(xr[0][t][e] & 0xFFFFu)), hi = h2f((uint16_t)(xr[0][t][e] >> 16));
         ss += lo * lo;
         ss += hi * hi;
@@ -313,7 +327,6 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
       }
   }
 
-  const bool last_live = (uint32_t)(tid + T * (UPL - 1)) < U;
   float acc[R][NM][NB];
 #pragma unroll
   for (int r = 0; r < R; r++) {
@@ -366,7 +379,10 @@ __global__ __launch_bounds__(512) void k_gemv_tile(GemvArgs a) {
       for (int w = 0; w < W; w++) s[m] += part[((w * R + r) * NM + m) * NB + b];
     }
     if (row < N && (uint32_t)b < a.nb) {
-      if constexpr (DUAL)
+      if constexpr (DUAL && (EPI & kEpiPair) != 0) {
+        a.y[row] = f2h(s[0]);
+        a.y2[row] = f2h(s[NM - 1]);
+      } else if constexpr (DUAL)
         a.y[row] = swiglu_h(s[0], s[NM - 1]);
       else if constexpr ((EPI & kEpiResid) != 0)
         a.y[row] = f2h(h2f(f2h(s[0])) + h2f(a.y[row]));

@@ -251,7 +251,7 @@ int prism_hip_model_set_embedding(prism_hip_model* m, const prism_hip_weight* em
   prism_hip_ctx* ctx = m->ctx;
   if ((rc = check_w4(ctx, embed, "embedding", m->cfg.vocab, m->cfg.hidden))) return rc;
   DeviceGuard g(m->device);
-  HIP_TRY(ctx, hipMemcpyAsync(m->embed, embed->d, embed->bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  if ((rc = copy_split_rows(ctx, embed, m->embed, m->embed + (size_t)m->cfg.vocab * 32, ctx->stream))) return rc;
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   m->embed_set = true;
   model_invalidate(m);
@@ -282,15 +282,15 @@ int prism_hip_model_set_layer(prism_hip_model* m, uint32_t layer, const prism_hi
   size_t lut_off = 0, idx_off = (size_t)m->nqkv * 32;
   for (const prism_hip_weight* w : parts) {
     const size_t lb = (size_t)w->dim_m * 32, ib = (size_t)w->dim_m * (D / 2);
-    HIP_TRY(ctx, hipMemcpyAsync(f + lut_off, w->d, lb, hipMemcpyDeviceToDevice, st));
-    HIP_TRY(ctx, hipMemcpyAsync(f + idx_off, w->d + lb, ib, hipMemcpyDeviceToDevice, st));
+    if ((rc = copy_split_rows(ctx, w, f + lut_off, f + idx_off, st))) return rc;
     lut_off += lb;
     idx_off += ib;
   }
-  HIP_TRY(ctx, hipMemcpyAsync(m->o[layer], o_proj->d, o_proj->bytes, hipMemcpyDeviceToDevice, st));
-  HIP_TRY(ctx, hipMemcpyAsync(m->gate[layer], gate_proj->d, gate_proj->bytes, hipMemcpyDeviceToDevice, st));
-  HIP_TRY(ctx, hipMemcpyAsync(m->up[layer], up_proj->d, up_proj->bytes, hipMemcpyDeviceToDevice, st));
-  HIP_TRY(ctx, hipMemcpyAsync(m->down[layer], down_proj->d, down_proj->bytes, hipMemcpyDeviceToDevice, st));
+  // the other projections keep their own split-block buffers
+  const prism_hip_weight* own[4] = {o_proj, gate_proj, up_proj, down_proj};
+  uint8_t* dst[4] = {m->o[layer], m->gate[layer], m->up[layer], m->down[layer]};
+  for (int i = 0; i < 4; i++)
+    if ((rc = copy_split_rows(ctx, own[i], dst[i], dst[i] + (size_t)own[i]->dim_m * 32, st))) return rc;
   HIP_TRY(ctx, hipStreamSynchronize(st));
   m->layer_set[layer] = true;
   model_invalidate(m);

@@ -20,6 +20,7 @@
 #include "gemm_kernels.hpp"
 #include "gemv_kernels.hpp"
 #include "gemv_tile.hpp"
+#include "gemv_lpr.hpp"
 #include "gemv_mfma.hpp"
 #include "palette_kernels.hpp"
 #include "step_kernels.hpp"
@@ -48,14 +49,20 @@ struct prism_hip_ctx {
 // Defined with prism_hip_model (model_step.hpp): forget the context.
 static void model_detach(prism_hip_model* m);
 
+// A weight's device copy is either the split-block payload as uploaded or,
+// for 4-bit matrices the lane-per-row GEMV covers in one round of row groups,
+// the GI64 layout (gemv_lpr.hpp: the same bytes regrouped per 64 rows, each
+// group's LUTs before its index chunks).  Kernels over GI64 take the base
+// pointer as both their LUT and their index pointer.
 struct prism_hip_weight {
   prism_hip_ctx* ctx = nullptr;
   int device = 0;
   uint32_t dim_m = 0, dim_n = 0, bits = 0, layout = 0;
-  size_t bytes = 0;
+  size_t bytes = 0;  // payload bytes as uploaded (split-block)
+  bool gi64 = false;
   uint8_t* d = nullptr;
   const uint8_t* lut() const { return d; }
-  const uint8_t* idx() const { return d + (size_t)dim_m * (2u << bits); }
+  const uint8_t* idx() const { return gi64 ? d : d + (size_t)dim_m * (2u << bits); }
 };
 
 namespace {
@@ -140,6 +147,20 @@ hipStream_t pick_stream(prism_hip_ctx* ctx, void* stream) {
   return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
 }
 
+// GI64 device layout (gemv_lpr.hpp) for 4-bit matrices whose row groups
+// fill between half and all of the CUs in one round (one 64-row group per
+// workgroup; the gate/up form holds two 64 KB table sets, one workgroup per
+// CU), with rows of at least 2048 elements.  MI355X, against k_gemv_tile on
+// split-block weights: 14336 x 4096 7.2 against 8.4 us, gate + up 2 x 14336
+// x 4096 12.3 us; 4864 x 896 3.5 against 3.05 us and 896 x 4864 6.3 against
+// 3.2 us (too few groups), 2 x 18944 x 3584 19.6 against 17.6 us (two
+// rounds), so those stay split-block.
+bool gi64_layout(const prism_hip_ctx* ctx, uint32_t dm, uint32_t dn, uint32_t bits) {
+  const uint32_t groups = (dm + prism::kGiRows - 1) / prism::kGiRows;
+  return bits == 4 && dn % 64 == 0 && dn >= 2048 && 2 * groups >= (uint32_t)ctx->num_cu &&
+         groups <= (uint32_t)ctx->num_cu && prism::gi64_bytes(dm, dn) < (1ull << 31);
+}
+
 // ---------------------------------------------------------------- GEMV plan
 // k_gemv_tile (gemv_tile.hpp) for K % 8 == 0 with 16-byte aligned x, in
 // passes of up to 8 batch vectors (the matrix-core kernel of gemv_mfma.hpp
@@ -194,7 +215,7 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
   const uint32_t U = K / 8;
   const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
   if (dual && NB != 1) return TilePlan{};
-  if (epi && (NB != 1 || bits != 4)) return TilePlan{};
+  if (epi == prism::kEpiPair ? !dual : epi && (NB != 1 || bits != 4)) return TilePlan{};
   const uint32_t uplmax = (uint32_t)(16 / NB < 8 ? 16 / NB : 8);
   // Very tall single-vector 4-bit matrices (an LM head: N >= 32768) take 4
   // rows per wave: at 2 rows, dispatching N/2 workgroups costs more than
@@ -224,6 +245,7 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
     if (pair) {
       if (dual) {
         if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, true, 1, prism::kEpiNorm, 2>(upl, threads);
+        if (epi == prism::kEpiPair) return tile_pick_upl<4, 2, true, 1, prism::kEpiPair, 2>(upl, threads);
         if (epi) return TilePlan{};
         return tile_pick_upl<4, 2, true, 1, 0, 2>(upl, threads);
       }
@@ -236,6 +258,7 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
     }
     if (dual) {
       if (epi == prism::kEpiNorm) return tile_pick_upl<4, 2, true, 1, prism::kEpiNorm>(upl, threads);
+      if (epi == prism::kEpiPair) return tile_pick_upl<4, 2, true, 1, prism::kEpiPair>(upl, threads);
       if (epi) return TilePlan{};
       return tile_pick_upl<4, 2, true, 1>(upl, threads);
     }
@@ -265,7 +288,10 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
       default: return tile_pick_upl<4, 4, false, 8>(upl, threads);
     }
   }
-  if (dual) return tile_pick_upl<8, 2, true, 1>(upl, threads);
+  if (dual) {
+    if (epi == prism::kEpiPair) return tile_pick_upl<8, 2, true, 1, prism::kEpiPair>(upl, threads);
+    return tile_pick_upl<8, 2, true, 1>(upl, threads);
+  }
   switch (NB) {
     case 1: return tile_pick_upl<8, 4, false, 1>(upl, threads);
     case 2: return tile_pick_upl<8, 4, false, 2>(upl, threads);
@@ -275,17 +301,22 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
 }
 
 // GEMV over raw split-block device pointers (lut2/idx2 non-null: gate+up
-// with the SwiGLU epilogue).  `epi` selects the decode step's fused norm /
-// residual forms, which have no generic fallback.
+// with the SwiGLU epilogue, or with d_y2 non-null the two raw outputs).
+// `epi` selects the decode step's fused norm / residual forms, which have no
+// generic fallback.
 int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, const uint8_t* lut,
                     const uint8_t* idx, const uint8_t* lut2, const uint8_t* idx2, const void* d_x, uint32_t nb,
-                    void* d_y, hipStream_t st, int epi = 0, float eps = 0.0f, const float* xpart = nullptr) {
+                    void* d_y, hipStream_t st, int epi = 0, float eps = 0.0f, const float* xpart = nullptr,
+                    void* d_y2 = nullptr) {
   const bool dual = (lut2 != nullptr);
+  const bool pair = dual && d_y2 != nullptr;
+  if (pair) epi = prism::kEpiPair;
   prism::GemvArgs a;
   a.lut = lut;
   a.idx = idx;
   a.lut2 = lut2;
   a.idx2 = idx2;
+  a.y2 = reinterpret_cast<uint16_t*>(d_y2);
   a.N = N;
   a.K = K;
   a.eps = eps;
@@ -337,14 +368,17 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
       const uint32_t grid = (N + (uint32_t)p.R - 1) / (uint32_t)p.R;
       HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(p.threads), args, p.lds, st));
     } else {
-      if (epi) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no fused kernel for %u-bit %ux%u", bits, N, K);
+      if (epi && !pair) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no fused kernel for %u-bit %ux%u", bits, N, K);
       const void* fn;
-      if (dual)
-        fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, true>)
-                       : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, true>);
+      if (pair)
+        fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, prism::kGenPair>)
+                       : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, prism::kGenPair>);
+      else if (dual)
+        fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, prism::kGenSwiglu>)
+                       : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, prism::kGenSwiglu>);
       else
-        fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, false>)
-                       : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, false>);
+        fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, prism::kGenSingle>)
+                       : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, prism::kGenSingle>);
       HIP_TRY(ctx, hipLaunchKernel(fn, dim3(N), dim3(64), args, 0, st));
     }
     b0 += chunk;
@@ -352,10 +386,98 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
   return PRISM_HIP_OK;
 }
 
+// GEMV over GI64 weights (w2: gate + up, SwiGLU or with d_y2 the pair).
+// One or two vectors a pass: k_gemv_lpr; three or more: the matrix-core
+// kernel (K % 128 == 0) in passes of up to 16, else lane-per-row passes of
+// two.  x not 16-byte aligned: the generic kernel.
+int launch_gemv_gi64(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
+                     uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
+  const uint32_t N = w->dim_m, K = w->dim_n;
+  const bool aligned = reinterpret_cast<uintptr_t>(d_x) % 16 == 0;
+  const dim3 groups((N + prism::kGiRows - 1) / prism::kGiRows);
+  if (w2) {
+    if (aligned) {
+      prism::LprArgs a{};
+      a.w = w->d;
+      a.w2 = w2->d;
+      a.x = reinterpret_cast<const uint16_t*>(d_x);
+      a.y = reinterpret_cast<uint16_t*>(d_y);
+      a.y2 = reinterpret_cast<uint16_t*>(d_y2);
+      a.N = N;
+      a.K = K;
+      a.nb = 1;
+      // the pair form splits K over the waves as the one-matrix GEMV does
+      // (8 waves), so each output is that GEMV's bit for bit
+      if (d_y2)
+        hipLaunchKernelGGL((prism::k_gemv_lpr<8, 2, 1, prism::kLprPair>), groups, dim3(512), 0, st, a);
+      else
+        hipLaunchKernelGGL((prism::k_gemv_lpr<16, 2, 1, prism::kLprSwiglu>), groups, dim3(1024), 0, st, a);
+    } else {
+      prism::GemvArgs a{};
+      a.lut = a.idx = w->d;
+      a.lut2 = a.idx2 = w2->d;
+      a.x = reinterpret_cast<const uint16_t*>(d_x);
+      a.y = reinterpret_cast<uint16_t*>(d_y);
+      a.y2 = reinterpret_cast<uint16_t*>(d_y2);
+      a.N = N;
+      a.K = K;
+      a.nb = 1;
+      if (d_y2)
+        hipLaunchKernelGGL((prism::k_gemv_generic<4, prism::kGenPair, true>), dim3(N), dim3(64), 0, st, a);
+      else
+        hipLaunchKernelGGL((prism::k_gemv_generic<4, prism::kGenSwiglu, true>), dim3(N), dim3(64), 0, st, a);
+    }
+    HIP_TRY(ctx, hipGetLastError());
+    return PRISM_HIP_OK;
+  }
+  for (uint32_t b0 = 0; b0 < nb;) {
+    const uint16_t* x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
+    uint16_t* y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
+    const uint32_t left = nb - b0;
+    uint32_t chunk;
+    if (!aligned) {
+      prism::GemvArgs a{};
+      a.lut = a.idx = w->d;
+      a.x = x;
+      a.y = y;
+      a.N = N;
+      a.K = K;
+      a.nb = chunk = left;
+      hipLaunchKernelGGL((prism::k_gemv_generic<4, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, a);
+    } else if (left >= 3 && K % prism::kGmGroup == 0) {
+      prism::GemvArgs a{};
+      a.lut = a.idx = w->d;
+      a.x = x;
+      a.y = y;
+      a.N = N;
+      a.K = K;
+      a.nb = chunk = left < (uint32_t)prism::kGmMaxNb ? left : (uint32_t)prism::kGmMaxNb;
+      hipLaunchKernelGGL((prism::k_gemv_mfma<4, true>), dim3((N + prism::kGmRows - 1) / prism::kGmRows),
+                         dim3(64 * prism::kGmWaves), 0, st, a);
+    } else {
+      prism::LprArgs a{};
+      a.w = w->d;
+      a.x = x;
+      a.y = y;
+      a.N = N;
+      a.K = K;
+      a.nb = chunk = left >= 2 ? 2u : 1u;
+      if (chunk == 2)
+        hipLaunchKernelGGL((prism::k_gemv_lpr<8, 1, 2, prism::kLprPlain>), groups, dim3(512), 0, st, a);
+      else
+        hipLaunchKernelGGL((prism::k_gemv_lpr<8, 1, 1, prism::kLprPlain>), groups, dim3(512), 0, st, a);
+    }
+    HIP_TRY(ctx, hipGetLastError());
+    b0 += chunk;
+  }
+  return PRISM_HIP_OK;
+}
+
 int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
-                uint32_t nb, void* d_y, hipStream_t st) {
+                uint32_t nb, void* d_y, hipStream_t st, void* d_y2 = nullptr) {
+  if (w->gi64) return launch_gemv_gi64(ctx, w, w2, d_x, nb, d_y, d_y2, st);
   return launch_gemv_raw(ctx, w->bits, w->dim_m, w->dim_n, w->lut(), w->idx(), w2 ? w2->lut() : nullptr,
-                         w2 ? w2->idx() : nullptr, d_x, nb, d_y, st);
+                         w2 ? w2->idx() : nullptr, d_x, nb, d_y, st, 0, 0.0f, nullptr, d_y2);
 }
 
 // One GEMM kernel launch over (tiles, splits) blocks, kernel signature
@@ -441,14 +563,14 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
       (uint64_t)bm * K * 2 < (1ull << 31)) {
     const uint32_t tiles4 = ((M + bm - 1) / bm) * ntn;
     const void* fn;
+#define PRISM_W4(MI_, SP_)                                                                   \
+  (w->gi64 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<MI_, SP_, true>)                \
+           : reinterpret_cast<const void*>(&prism::k_gemm_w4<MI_, SP_, false>))
     if (nsplit > 1)
-      fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2, true>)
-           : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4, true>)
-                     : reinterpret_cast<const void*>(&prism::k_gemm_w4<8, true>);
+      fn = mi == 2 ? PRISM_W4(2, true) : mi == 4 ? PRISM_W4(4, true) : PRISM_W4(8, true);
     else
-      fn = mi == 2   ? reinterpret_cast<const void*>(&prism::k_gemm_w4<2, false>)
-           : mi == 4 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<4, false>)
-                     : reinterpret_cast<const void*>(&prism::k_gemm_w4<8, false>);
+      fn = mi == 2 ? PRISM_W4(2, false) : mi == 4 ? PRISM_W4(4, false) : PRISM_W4(8, false);
+#undef PRISM_W4
     return launch_gemm_blocks(ctx, fn, tiles4, nsteps, nsplit, w, d_X, M, d_Y, st);
   }
   // 8-bit, K % 64 == 0, more than 256 rows: 256 x 128 blocks over a 64-wide
@@ -475,6 +597,8 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
       return launch_gemm_blocks(ctx, fn, tiles8, nsteps, nsplit8, w, d_X, M, d_Y, st);
     }
   }
+  // GI64 weights (K % 64 == 0, below 2 GiB) always take k_gemm_w4 above.
+  if (w->gi64) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no GEMM kernel for this GI64 weight (%ux%u)", N, K);
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
   const uint8_t* lut = w->lut();
   const uint8_t* idx = w->idx();
@@ -498,9 +622,28 @@ int launch_decode(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, 
   uint32_t N = w->dim_m, K = w->dim_n;
   uint16_t* out = reinterpret_cast<uint16_t*>(d_out);
   void* args[] = {&lut, &idx, &N, &K, &row0, &nrows, &out};
-  const void* fn = w->bits == 4 ? reinterpret_cast<const void*>(&prism::k_decode_rows<4>)
-                                : reinterpret_cast<const void*>(&prism::k_decode_rows<8>);
+  const void* fn = w->bits == 8 ? reinterpret_cast<const void*>(&prism::k_decode_rows<8>)
+                   : w->gi64    ? reinterpret_cast<const void*>(&prism::k_decode_rows<4, true>)
+                                : reinterpret_cast<const void*>(&prism::k_decode_rows<4>);
   HIP_TRY(ctx, hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(256), args, 0, st));
+  return PRISM_HIP_OK;
+}
+
+// A 4-bit weight's LUT block and index rows in split-block form at dst_lut
+// ([N][32] B) and dst_idx ([N][K/2] B), on stream st: copies, or for a GI64
+// weight the inverse regrouping.
+int copy_split_rows(prism_hip_ctx* ctx, const prism_hip_weight* w, uint8_t* dst_lut, uint8_t* dst_idx,
+                    hipStream_t st) {
+  const uint32_t N = w->dim_m, K = w->dim_n;
+  if (!w->gi64) {
+    HIP_TRY(ctx, hipMemcpyAsync(dst_lut, w->lut(), (size_t)N * 32, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(ctx, hipMemcpyAsync(dst_idx, w->idx(), (size_t)N * (K / 2), hipMemcpyDeviceToDevice, st));
+    return PRISM_HIP_OK;
+  }
+  const size_t pieces = (size_t)N * (2 + K / 32);
+  const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
+  hipLaunchKernelGGL(prism::k_gi64_unpack, dim3(grid), dim3(256), 0, st, w->d, dst_lut, dst_idx, N, K);
+  HIP_TRY(ctx, hipGetLastError());
   return PRISM_HIP_OK;
 }
 
@@ -597,10 +740,31 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
   w->bits = bits;
   w->layout = layout;
   w->bytes = bytes;
-  hipError_t e = hipMalloc(&w->d, bytes);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(w->d, src, bytes, src_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
+  w->gi64 = gi64_layout(ctx, dm, dn, bits);
+  hipError_t e = hipMalloc(&w->d, w->gi64 ? prism::gi64_bytes(dm, dn) : bytes);
+  void* tmp = nullptr;
+  if (!w->gi64) {
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(w->d, src, bytes, src_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
+  } else {
+    // regroup the split-block payload on the device (a host payload is
+    // staged in a temporary device buffer first)
+    const void* s = src;
+    if (e == hipSuccess && !src_dev) {
+      e = hipMalloc(&tmp, bytes);
+      if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+      s = tmp;
+    }
+    if (e == hipSuccess) {
+      const size_t pieces = prism::gi64_bytes(dm, dn) / 16;
+      const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
+      hipLaunchKernelGGL(prism::k_gi64_pack, dim3(grid), dim3(256), 0, ctx->stream,
+                         reinterpret_cast<const uint8_t*>(s), w->d, dm, dn);
+      e = hipGetLastError();
+    }
+  }
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (tmp) (void)hipFree(tmp);
   if (e != hipSuccess) {
     fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload (%zu bytes): %s", bytes, hipGetErrorString(e));
     if (w->d) (void)hipFree(w->d);
@@ -709,6 +873,39 @@ int prism_hip_gateup_swiglu(prism_hip_ctx* ctx, const prism_hip_weight* gate, co
   HIP_TRY(ctx, hipMemcpyAsync(st, x, xb, hipMemcpyHostToDevice, ctx->stream));
   if ((rc = launch_gemv(ctx, gate, up, st, 1, st + yoff, ctx->stream))) return rc;
   HIP_TRY(ctx, hipMemcpyAsync(y, st + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+// ---- gate and up without the activation: two outputs
+int prism_hip_gate_up_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up,
+                          const void* d_x, void* d_gate_out, void* d_up_out, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_pair(ctx, gate, up);
+  if (rc) return rc;
+  if (!d_x || !d_gate_out || !d_up_out) return fail(ctx, PRISM_HIP_ERR_NULL, "x or an output is NULL");
+  DeviceGuard g(ctx->device);
+  rc = launch_gemv(ctx, gate, up, d_x, 1, d_gate_out, pick_stream(ctx, stream), d_up_out);
+  if (rc == PRISM_HIP_OK) ctx->err.clear();
+  return rc;
+}
+
+int prism_hip_gate_up(prism_hip_ctx* ctx, const prism_hip_weight* gate, const prism_hip_weight* up, const uint16_t* x,
+                      uint16_t* gate_out, uint16_t* up_out) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_pair(ctx, gate, up);
+  if (rc) return rc;
+  if (!x || !gate_out || !up_out) return fail(ctx, PRISM_HIP_ERR_NULL, "x or an output is NULL");
+  DeviceGuard g(ctx->device);
+  const size_t xb = (size_t)gate->dim_n * 2, yb = (size_t)gate->dim_m * 2;
+  const size_t yoff = (xb + 255) & ~(size_t)255, y2off = yoff + ((yb + 255) & ~(size_t)255);
+  if ((rc = ensure_stage(ctx, y2off + yb))) return rc;
+  uint8_t* st = reinterpret_cast<uint8_t*>(ctx->d_stage);
+  HIP_TRY(ctx, hipMemcpyAsync(st, x, xb, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = launch_gemv(ctx, gate, up, st, 1, st + yoff, ctx->stream, st + y2off))) return rc;
+  HIP_TRY(ctx, hipMemcpyAsync(gate_out, st + yoff, yb, hipMemcpyDeviceToHost, ctx->stream));
+  HIP_TRY(ctx, hipMemcpyAsync(up_out, st + y2off, yb, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
   ctx->err.clear();
   return PRISM_HIP_OK;

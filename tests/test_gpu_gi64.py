@@ -1,0 +1,241 @@
+"""The GI64 device layout (4-bit weights whose 64-row groups fill 128..256
+CUs with rows of >= 2048 elements, K % 64 == 0) and the two-output gate/up
+GEMV, through the C ABI against the CPU oracle.
+
+Every operation on a weight must give the same results whatever device
+layout the library chose for it: the lane-per-row GEMV (1..2 vectors), the
+matrix-core GEMV over GI64 (3+ vectors), the generic kernel (unaligned x),
+the GEMM, the row decode and the decode-step model's copies.  Shapes:
+14336 x 4096 (224 groups), 9000 x 2048 (141 groups, a ragged last group),
+8192 x 2112 (K % 128 != 0: no matrix-core pass), 16384 x 2048 (256 groups).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+GI64_SHAPES = [(14336, 4096), (9000, 2048), (8192, 2112), (16384, 2048)]
+
+
+def _rel(y, ref):
+    a = np.asarray(y).view(np.float16).astype(np.float64)
+    r = np.asarray(ref).view(np.float16).astype(np.float64)
+    den = np.max(np.abs(r))
+    return float(np.max(np.abs(a - r)) / den) if den > 0 else float(np.max(np.abs(a)))
+
+
+def _check(y, ref, what):
+    y = np.asarray(y).reshape(-1, np.asarray(ref).shape[-1])
+    ref = np.asarray(ref).reshape(y.shape)
+    for b in range(y.shape[0]):
+        err = _rel(y[b], ref[b])
+        assert err <= TOL, f"{what}: vector {b} rel err {err:.3e}"
+
+
+def _gi64(N, K, bits=4, num_cu=256):
+    groups = (N + 63) // 64
+    return bits == 4 and K % 64 == 0 and K >= 2048 and 2 * groups >= num_cu and groups <= num_cu
+
+
+@pytest.mark.parametrize("N,K", GI64_SHAPES)
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 16])
+def test_gi64_gemv(pe, oracle, gpu_ctx, N, K, batch):
+    assert _gi64(N, K)
+    if N * K > 4 * 10**7 and batch in (3, 5):
+        pytest.skip("odd batches covered at the smaller shapes")
+    t = pe.synth_tensor(N, K, 4, seed=N + K + batch)
+    x = pe.synth_x(batch, K, seed=batch * 3 + 1)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi64 gemv {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    ref = oracle.gemv(x, t.payload, N, K, 4, threads=8)
+    _check(y, ref, f"GI64 {N}x{K} batch {batch}")
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
+def test_gi64_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
+    """One-hot x: every output is the decoded weight itself, LUT_r[idx(r, k)],
+    through the lane-per-row GEMV (one vector) and the matrix-core GEMV
+    over GI64 (six vectors at once)."""
+    t = pe.synth_tensor(N, K, 4, seed=K + 11)
+    lut, idx = pe.unpack_payload(t.payload, N, K, 4)
+    ks = [0, 1, 31, 32, K // 2 + 5, K - 1]
+    x = np.zeros((len(ks), K), dtype=np.float16)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    w = gpu_ctx.upload_tensor(t)
+    ys = gpu_ctx.gemv(w, x.view(np.uint16))
+    for i, k in enumerate(ks):
+        want = lut[np.arange(N), idx[:, k]]
+        want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
+        y1 = gpu_ctx.gemv(w, x[i:i + 1].view(np.uint16))[0]
+        assert np.array_equal(y1, want), f"column {k}, one vector"
+        assert np.array_equal(ys[i], want), f"column {k}, six vectors"
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
+def test_gi64_unaligned_x(pe, oracle, gpu_ctx, N, K):
+    """x not 16-byte aligned: the generic kernel reads GI64 as well."""
+    import torch
+    t = pe.synth_tensor(N, K, 4, seed=N - K)
+    x = pe.synth_x(2, K, seed=5)
+    w = gpu_ctx.upload_tensor(t)
+    buf = torch.zeros(2 * K + 8, dtype=torch.int16, device="cuda")
+    buf[1:1 + 2 * K] = torch.from_numpy(x.reshape(-1).view(np.int16)).cuda()
+    dx = buf[1:]
+    dy = torch.empty(2 * N, dtype=torch.int16, device="cuda")
+    gpu_ctx.gemv_dev(w, dx, 2, dy)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy().view(np.uint16).reshape(2, N)
+    _check(y, oracle.gemv(x, t.payload, N, K, 4, threads=8), f"GI64 {N}x{K} unaligned x")
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
+def test_gi64_decode_rows(pe, oracle, gpu_ctx, N, K):
+    """Row decode and lut_embed over GI64 are the oracle's bytes exactly,
+    including rows of the ragged last group."""
+    import torch
+    t = pe.synth_tensor(N, K, 4, seed=3 * N + 1)
+    w = gpu_ctx.upload_tensor(t)
+    for r0, nr in [(0, 3), (63, 2), (N - 5, 5), (N // 2, 64)]:
+        out = torch.empty(nr * K, dtype=torch.int16, device="cuda")
+        gpu_ctx.decode_rows_dev(w, r0, nr, out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(np.uint16).reshape(nr, K)
+        want = oracle.decode_rows(t.payload, N, K, 4, r0, nr)
+        assert np.array_equal(got, want), f"rows {r0}..{r0 + nr}"
+    for tok in (0, 64, N - 1):
+        assert np.array_equal(gpu_ctx.lut_embed(w, tok), oracle.lut_embed(tok, t.payload, N, K)), f"token {tok}"
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
+def test_gi64_upload_dev(pe, gpu_ctx, N, K):
+    """A device-side payload is regrouped the same way as a host one."""
+    import torch
+    t = pe.synth_tensor(N, K, 4, seed=N * 2 + K)
+    x = pe.synth_x(1, K, seed=9)
+    w_host = gpu_ctx.upload_tensor(t)
+    dpay = torch.from_numpy(t.payload.view(np.int8)).cuda()
+    w_dev = gpu_ctx.upload_dev(dpay, N, K, 4)
+    assert np.array_equal(gpu_ctx.gemv(w_host, x), gpu_ctx.gemv(w_dev, x))
+    w_host.free()
+    w_dev.free()
+
+
+# (bits, N, K): split-block shapes of every tile form (one-wave tiles, two
+# per workgroup, 8-bit), config 2's matrix, ragged K (generic kernel), and
+# GI64 shapes (the lane-per-row kernel's pair form)
+PAIR_SHAPES = [(4, 4864, 896), (4, 18944, 3584), (4, 300, 4096), (8, 300, 512), (8, 14336, 4096),
+               (4, 7, 40), (8, 9, 7), (4, 14336, 4096), (4, 9000, 2048)]
+
+
+@pytest.mark.parametrize("bits,N,K", PAIR_SHAPES)
+def test_gate_up_pair(pe, oracle, gpu_ctx, bits, N, K):
+    """prism_hip_gate_up: both raw outputs equal separate GEMVs bit for bit
+    (same kernels, same summation order) and the oracle within tolerance."""
+    tg = pe.synth_tensor(N, K, bits, seed=N + 1)
+    tu = pe.synth_tensor(N, K, bits, seed=N + 2)
+    x = pe.synth_x(1, K, seed=N + 3)
+    wg, wu = gpu_ctx.upload_tensor(tg), gpu_ctx.upload_tensor(tu)
+    print(f"gate_up pair {bits}-bit {N}x{K}", flush=True)
+    yg, yu = gpu_ctx.gate_up(wg, wu, x)
+    assert np.array_equal(yg, gpu_ctx.gemv(wg, x)[0]), "gate output differs from its GEMV"
+    assert np.array_equal(yu, gpu_ctx.gemv(wu, x)[0]), "up output differs from its GEMV"
+    _check(yg, oracle.gemv(x, tg.payload, N, K, bits, threads=8), "gate")
+    _check(yu, oracle.gemv(x, tu.payload, N, K, bits, threads=8), "up")
+    wg.free()
+    wu.free()
+
+
+def test_gate_up_pair_dev_and_errors(pe, gpu_ctx):
+    """The device form on a torch stream matches the host form; shape and
+    NULL checks return the documented codes."""
+    import torch
+    from importlib import import_module
+    nat = import_module("prism-engine_amd._native")
+    N, K = 14336, 4096
+    tg, tu = pe.synth_tensor(N, K, 4, seed=1), pe.synth_tensor(N, K, 4, seed=2)
+    x = pe.synth_x(1, K, seed=3)
+    wg, wu = gpu_ctx.upload_tensor(tg), gpu_ctx.upload_tensor(tu)
+    yg, yu = gpu_ctx.gate_up(wg, wu, x)
+    s = torch.cuda.Stream()
+    dx = torch.from_numpy(x.view(np.int16)).cuda()
+    dg = torch.empty(N, dtype=torch.int16, device="cuda")
+    du = torch.empty(N, dtype=torch.int16, device="cuda")
+    gpu_ctx.gate_up_dev(wg, wu, dx, dg, du, stream=s)
+    s.synchronize()
+    assert np.array_equal(dg.cpu().numpy().view(np.uint16), yg)
+    assert np.array_equal(du.cpu().numpy().view(np.uint16), yu)
+    small = gpu_ctx.upload_tensor(pe.synth_tensor(64, K, 4, seed=4))
+    with pytest.raises(nat.PrismHipError) as e:
+        gpu_ctx.gate_up(wg, small, x)
+    assert e.value.code == nat.ERR_MISMATCH
+    lib = nat.load()
+    assert lib.prism_hip_gate_up(gpu_ctx.h, wg.h, wu.h, None, None, None) == nat.ERR_NULL
+    for w in (wg, wu, small):
+        w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
+def test_gi64_gateup_swiglu(pe, oracle, gpu_ctx, N, K):
+    tg = pe.synth_tensor(N, K, 4, seed=N + 5)
+    tu = pe.synth_tensor(N, K, 4, seed=N + 6)
+    x = pe.synth_x(1, K, seed=N + 7)
+    wg, wu = gpu_ctx.upload_tensor(tg), gpu_ctx.upload_tensor(tu)
+    y = gpu_ctx.gateup_swiglu(wg, wu, x)
+    ref = oracle.gateup_swiglu(x[0], tg.payload, tu.payload, N, K, 4, threads=8)
+    _check(y, ref, f"GI64 gate_up + SwiGLU {N}x{K}")
+    wg.free()
+    wu.free()
+
+
+@pytest.mark.parametrize("M", [24, 64, 200, 300])
+def test_gi64_gemm(pe, oracle, gpu_ctx, M):
+    """Prefill GEMM over GI64 weights with a ragged last group: GEMV passes
+    (24 rows), split K (64, 200) and whole-K blocks (300); every row checked
+    against the float32 product of the decoded weights, a spread of rows
+    against the oracle."""
+    N, K = 9000, 2048
+    t = pe.synth_tensor(N, K, 4, seed=M + 40)
+    X = pe.synth_x(M, K, seed=M + 41)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi64 gemm M={M}", flush=True)
+    Y = gpu_ctx.gemm(w, X)
+    dense = oracle.decode_rows(t.payload, N, K, 4, 0, N).view(np.float16).astype(np.float32)
+    Yf = X.view(np.float16).astype(np.float32) @ dense.T
+    got = Y.view(np.float16).astype(np.float32)
+    for m in range(M):
+        err = np.max(np.abs(got[m] - Yf[m])) / np.max(np.abs(Yf[m]))
+        assert err <= TOL, f"row {m}: {err:.3e}"
+    rows = sorted(set([0, M // 3, M // 2, M - 1]))
+    ref = oracle.gemm(np.ascontiguousarray(X[rows]), t.payload, N, K, 4, threads=8)
+    for i, m in enumerate(rows):
+        assert _rel(Y[m], ref[i]) <= TOL
+    w.free()
+
+
+def test_gi64_model_step(pe, oracle, gpu_ctx):
+    """A decode-step model whose embedding (9000 x 2048) and gate/up
+    (8192 x 2048) weights were uploaded in the GI64 layout: the model's
+    split-block copies are regrouped back, and the step matches the oracle."""
+    cfg = pe.Qwen2Config(n_layers=1, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64, intermediate=8192,
+                         vocab=9000)
+    assert _gi64(cfg.vocab, cfg.hidden) and _gi64(cfg.intermediate, cfg.hidden)
+    embed, layers = pe.synth_weights(cfg, 21)
+    m = pe.Model.from_tensors(gpu_ctx, cfg, embed, layers, max_seq=16)
+    kv = oracle.KVState(cfg.n_layers, cfg.kv_dim, 16)
+    for l, (k, v) in enumerate(pe.synth_kv(cfg, 4, 21)):
+        m.kv_append(l, k, v)
+        for i in range(4):
+            kv.append(l, k[i], v[i])
+    got = m.step(77, 4)
+    emb_p, lay_p = pe.model.payloads(embed, layers)
+    want = oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv, 77, 4, threads=8)
+    err = _rel(got, want)
+    assert err <= TOL, f"logits rel err {err:.3e}"
+    m.close()
