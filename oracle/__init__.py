@@ -134,6 +134,8 @@ def lib():
                                          ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t),
                                          ctypes.c_uint32, ctypes.c_int64, _u16p, ctypes.c_int]
         L.cpuref_decode_step.restype = ctypes.c_int
+        L.cpuref_set_fold_mode.argtypes = [ctypes.c_int]
+        L.cpuref_set_fold_mode.restype = None
         _f32p = ctypes.POINTER(ctypes.c_float)
         L.cpuref_fit_palette.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _f32p]
         L.cpuref_fit_palette.restype = ctypes.c_size_t
@@ -355,13 +357,17 @@ class KVState:
 
 
 def decode_step(dims, eps: float, embed, layers, kv: KVState, token: int, pos: int,
-                threads: int = 1) -> np.ndarray:
+                threads: int = 1, fold: int = 0) -> np.ndarray:
     """PrismEngine::step (engine_impl.rs:1076-1405) for a Qwen2 graph.
 
     dims = (n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate,
     vocab, bits); `layers` is a list of 7-payload tuples (q, k, v, o, gate,
     up, down); `embed` the [vocab x hidden] 4-bit embedding (tied LM head).
-    Advances `kv` by one token per layer and returns the fp16 logits."""
+    Advances `kv` by one token per layer and returns the fp16 logits.
+
+    fold=1 runs the order-perturbed variant (prism_cpuref.c: every long sum
+    in 64-term blocks added as a tree) -- test support for measuring
+    summation-order drift, not the reference's arithmetic."""
     L = int(dims[0])
     assert len(layers) == L and len(kv.k) == L
     d = (ctypes.c_uint32 * 8)(*[int(v) for v in dims])
@@ -374,8 +380,13 @@ def decode_step(dims, eps: float, embed, layers, kv: KVState, token: int, pos: i
     lens = (ctypes.c_size_t * max(1, L))(*[int(v) for v in kv.len])
     embed = np.ascontiguousarray(embed, dtype=np.uint8)
     logits = np.zeros(int(dims[6]), dtype=np.uint16)
-    rc = lib().cpuref_decode_step(d, ctypes.c_float(eps), _p8(embed), wp, kp, vp, lens, token, pos,
-                                  _p16(logits), threads)
+    L_ = lib()
+    L_.cpuref_set_fold_mode(int(fold))
+    try:
+        rc = L_.cpuref_decode_step(d, ctypes.c_float(eps), _p8(embed), wp, kp, vp, lens, token, pos,
+                                   _p16(logits), threads)
+    finally:
+        L_.cpuref_set_fold_mode(0)
     assert rc == 0, rc
     for l in range(L):
         kv.len[l] = lens[l]

@@ -103,6 +103,51 @@ uint16_t cpuref_f32_to_f16(float f) {
   return (uint16_t)out;
 }
 
+/* ---- summation order (test support) -------------------------------------
+ * Mode 0 (the default) is the reference's sequential left fold, which every
+ * function in this file restates.  Mode 1 is an order-perturbed variant used
+ * only by tests/test_step_order.py to measure how far an equally valid fp32
+ * summation order moves the decode step's outputs: each long sum (the GEMV
+ * rows, the RMS norm's sum of squares, the softmax denominator and the
+ * attention's value sums) is cut into blocks of 64 consecutive terms, each
+ * block folded sequentially, and the block sums added as a binary tree --
+ * the shape of a GPU reduction.  It is not a restatement of anything. */
+int cpuref_fold_mode = 0;
+void cpuref_set_fold_mode(int mode) { cpuref_fold_mode = mode; }
+
+/* Blocked accumulator for mode 1: add terms in order, close a block every
+ * 64 terms, and finish with a pairwise tree over the block sums. */
+typedef struct {
+  float part[2048];
+  size_t nparts, cnt;
+  float acc;
+} cpuref_blocked;
+void cpuref_blocked_init(cpuref_blocked* b) {
+  b->nparts = 0;
+  b->cnt = 0;
+  b->acc = 0.0f;
+}
+void cpuref_blocked_add(cpuref_blocked* b, float v) {
+  b->acc += v;
+  if (++b->cnt == 64) {
+    if (b->nparts < 2048) b->part[b->nparts++] = b->acc;
+    b->acc = 0.0f;
+    b->cnt = 0;
+  }
+}
+float cpuref_blocked_sum(cpuref_blocked* b) {
+  if (b->cnt && b->nparts < 2048) b->part[b->nparts++] = b->acc;
+  size_t n = b->nparts;
+  if (n == 0) return 0.0f;
+  while (n > 1) {
+    const size_t h = n / 2;
+    for (size_t i = 0; i < h; i++) b->part[i] = b->part[2 * i] + b->part[2 * i + 1];
+    if (n & 1) b->part[h] = b->part[n - 1];
+    n = h + (n & 1);
+  }
+  return b->part[0];
+}
+
 /* ---- palettized GEMV ---------------------------------------------------- */
 
 static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
@@ -116,6 +161,15 @@ static uint16_t gemv4_row(const uint16_t* inp, const uint8_t* p, uint32_t dm, ui
   float cb[16];
   for (int i = 0; i < 16; i++) cb[i] = cpuref_f16_to_f32(rd16(p + (size_t)r * 32 + (size_t)i * 2));
   const size_t io = cbb + (size_t)r * (dn / 2);
+  if (cpuref_fold_mode == 1) {
+    cpuref_blocked b;
+    cpuref_blocked_init(&b);
+    for (uint32_t wi = 0; wi < dn / 8; wi++) {
+      uint32_t pw = rd32(p + io + (size_t)wi * 4);
+      for (uint32_t j = 0; j < 8; j++) cpuref_blocked_add(&b, cpuref_f16_to_f32(inp[wi * 8 + j]) * cb[(pw >> (j * 4)) & 0x0Fu]);
+    }
+    return cpuref_f32_to_f16(cpuref_blocked_sum(&b));
+  }
   float acc = 0.0f;
   for (uint32_t wi = 0; wi < dn / 8; wi++) {
     uint32_t pw = rd32(p + io + (size_t)wi * 4);
@@ -149,6 +203,13 @@ static uint16_t gemv8_row(const uint16_t* inp, const uint8_t* p, uint32_t dm, ui
   const size_t cbb = (size_t)dm * 256 * 2;
   const uint8_t* lut = p + (size_t)r * 512;
   const uint8_t* idx = p + cbb + (size_t)r * dn;
+  if (cpuref_fold_mode == 1) {
+    cpuref_blocked b;
+    cpuref_blocked_init(&b);
+    for (uint32_t k = 0; k < dn; k++)
+      cpuref_blocked_add(&b, cpuref_f16_to_f32(inp[k]) * cpuref_f16_to_f32(rd16(lut + (size_t)idx[k] * 2)));
+    return cpuref_f32_to_f16(cpuref_blocked_sum(&b));
+  }
   float acc = 0.0f;
   for (uint32_t k = 0; k < dn; k++) {
     acc += cpuref_f16_to_f32(inp[k]) * cpuref_f16_to_f32(rd16(lut + (size_t)idx[k] * 2));

@@ -46,13 +46,31 @@ void cpuref_lut_embed(uint32_t token, const uint8_t* payload, uint32_t vocab_siz
 #define F(h) cpuref_f16_to_f32(h)
 #define H(f) cpuref_f32_to_f16(f)
 
+/* Summation order switch and blocked accumulator (prism_cpuref.c). */
+extern int cpuref_fold_mode;
+typedef struct {
+  float part[2048];
+  size_t nparts, cnt;
+  float acc;
+} cpuref_blocked;
+void cpuref_blocked_init(cpuref_blocked* b);
+void cpuref_blocked_add(cpuref_blocked* b, float v);
+float cpuref_blocked_sum(cpuref_blocked* b);
+
 /* rms_norm_inplace: inv = 1 / sqrt(sum(f*f) / n + eps), sequential fp32
  * sum; x <- f16(x * inv). */
 void cpuref_rms_norm_inplace(uint16_t* x, size_t n, float eps) {
   float sum = 0.0f;
-  for (size_t i = 0; i < n; i++) {
-    float f = F(x[i]);
-    sum += f * f;
+  if (cpuref_fold_mode == 1) {
+    cpuref_blocked b;
+    cpuref_blocked_init(&b);
+    for (size_t i = 0; i < n; i++) cpuref_blocked_add(&b, F(x[i]) * F(x[i]));
+    sum = cpuref_blocked_sum(&b);
+  } else {
+    for (size_t i = 0; i < n; i++) {
+      float f = F(x[i]);
+      sum += f * f;
+    }
   }
   float inv = 1.0f / sqrtf(sum / (float)n + eps);
   for (size_t i = 0; i < n; i++) x[i] = H(F(x[i]) * inv);
@@ -131,14 +149,26 @@ void cpuref_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
     float mx = -INFINITY;
     for (size_t p = 0; p < sl; p++) mx = fmaxf(mx, sc[p]);
     float es = 0.0f;
-    for (size_t p = 0; p < sl; p++) {
-      ex[p] = expf(sc[p] - mx);
-      es += ex[p];
+    for (size_t p = 0; p < sl; p++) ex[p] = expf(sc[p] - mx);
+    if (cpuref_fold_mode == 1) {
+      cpuref_blocked b;
+      cpuref_blocked_init(&b);
+      for (size_t p = 0; p < sl; p++) cpuref_blocked_add(&b, ex[p]);
+      es = cpuref_blocked_sum(&b);
+    } else {
+      for (size_t p = 0; p < sl; p++) es += ex[p];
     }
     const float inv = 1.0f / (es + 1e-10f);
     for (size_t d = 0; d < hd; d++) {
       float ac = 0.0f;
-      for (size_t p = 0; p < sl; p++) ac += ex[p] * F(vc[p * kvd + kh * hd + d]) * inv;
+      if (cpuref_fold_mode == 1) {
+        cpuref_blocked b;
+        cpuref_blocked_init(&b);
+        for (size_t p = 0; p < sl; p++) cpuref_blocked_add(&b, ex[p] * F(vc[p * kvd + kh * hd + d]) * inv);
+        ac = cpuref_blocked_sum(&b);
+      } else {
+        for (size_t p = 0; p < sl; p++) ac += ex[p] * F(vc[p * kvd + kh * hd + d]) * inv;
+      }
       out[qb + d] = H(ac);
     }
   }

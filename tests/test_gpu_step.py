@@ -4,7 +4,8 @@ The oracle (oracle/prism_cpuref_step.c) restates PrismEngine::step
 (src/lut/engine_impl.rs:1076-1405) for the Qwen2 graph; its pinning is in
 test_step_oracle.py.  Bit-exact here: the INT8 KV blocks written by
 kv_append (KVCache::append).  Floating point: the logits of each step must
-be within STEP_TOL max relative error of the oracle's (the GPU sums the
+be within STEP_TOL max relative error of the oracle's, or the order-drift
+bound for deep models (the GPU sums the
 norm, the GEMV rows, the softmax and the attention output in a different
 order than the reference's sequential fp32 folds, and uses the device's
 expf; one fp16 ulp is ~1e-3 relative, and 24 layers of residual stream
@@ -20,11 +21,12 @@ import oracle
 pe = importlib.import_module("prism-engine_amd")
 pytestmark = pytest.mark.gpu
 
-# 2e-3 (the per-output-vector bound of a single GEMV) for shallow models;
-# 1e-2 for 24 layers, where per-GEMV ulp differences travel the residual
-# stream (measured 3.9e-3 on the Qwen2.5-0.5B step).
+# 2e-3, the per-output-vector bound of a single GEMV, for shallow models.
+# Deeper models are held to twice the spread that the summation order alone
+# causes at the same depth (tests/test_step_order.py: the reference's
+# sequential folds against a blocked tree order, both in the oracle), or
+# 2e-3 where that is larger.
 STEP_TOL = 2e-3
-STEP_TOL_DEEP = 1e-2
 TINY = dict(n_layers=2, hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, intermediate=256, vocab=300)
 
 
@@ -183,20 +185,42 @@ def test_step_errors(gpu_ctx):
         pe.Model(gpu_ctx, bad, max_seq=8)
 
 
-def test_step_qwen25_05b_matches_oracle(gpu_ctx):
-    """Config 3 at full size: 24 layers, 151936 x 896 tied LM head, 512
-    cached tokens (fp16 N(0,1) through the INT8 cache), one step at pos 512."""
+def test_step_depth_sweep(gpu_ctx):
+    """Error against depth.  Models of 1, 2, 4, 8, 16 and 24 layers (the
+    last is config 3: Qwen2.5-0.5B with its 151936 x 896 tied LM head) are
+    built from the same weights and the same 512 cached tokens (fp16 N(0,1)
+    through the INT8 cache), and one step at pos 512 is compared with the
+    sequential oracle.  At each depth the GPU's logits must lie within
+    max(2e-3, 2 x the oracle's own order drift at that depth), the 1- and
+    2-layer steps within 2e-3, and the error must not jump: it grows with
+    depth as the order drift does."""
+    import test_step_order as so
     cfg = pe.Qwen2Config()
-    print("qwen2.5-0.5b: building", flush=True)
-    m, emb_p, lay_p, kv = build(gpu_ctx, cfg, 1003, 512, max_seq=1024, capacity=600)
-    print("qwen2.5-0.5b: step", flush=True)
-    got = m.step(42, 512)
-    want = oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv, 42, 512, threads=16)
-    err = pe.rel_err(got, want)
-    print(f"qwen2.5-0.5b logits rel err {err:.3e}", flush=True)
-    assert err <= STEP_TOL_DEEP
-    # the argmax token agrees (greedy decoding, engine_impl.rs argmax)
-    g = got.view(np.float16).astype(np.float32)
-    w = want.view(np.float16).astype(np.float32)
-    assert int(np.argmax(g)) == int(np.argmax(w)) or abs(g.max() - w[np.argmax(g)]) < 1e-2
-    m.close()
+    depths = (1, 2, 4, 8, 16, 24)
+    print("depth sweep: oracle", flush=True)
+    drift = so.step_drift(cfg, depths)
+    embed, layers = pe.synth_weights(cfg, 1003)
+    kvs = pe.synth_kv(cfg, 512, 1003)
+    errs = {}
+    for L in depths:
+        cl = pe.Qwen2Config(n_layers=L)
+        print(f"depth sweep: {L} layers", flush=True)
+        m = pe.Model.from_tensors(gpu_ctx, cl, embed, layers[:L], max_seq=600)
+        for l in range(L):
+            m.kv_append(l, *kvs[l])
+        got = m.step(42, 512)
+        want, d = drift[L]
+        errs[L] = pe.rel_err(got, want)
+        print(f"depth {L:2d}: GPU vs oracle {errs[L]:.3e}, oracle order drift {d:.3e}", flush=True)
+        assert errs[L] <= max(STEP_TOL, 2.0 * d), f"{L} layers: {errs[L]:.3e} against drift {d:.3e}"
+        if L <= 2:
+            assert errs[L] <= STEP_TOL
+        if L == 24:
+            # the argmax token agrees (greedy decoding, engine_impl.rs argmax)
+            g = got.view(np.float16).astype(np.float32)
+            w = want.view(np.float16).astype(np.float32)
+            assert int(np.argmax(g)) == int(np.argmax(w)) or abs(g.max() - w[np.argmax(g)]) < 1e-2
+        m.close()
+    # no jump: each doubling of depth at most triples the error
+    for a, b in zip(depths, depths[1:]):
+        assert errs[b] <= 3.0 * max(errs[a], 1e-4), f"{a} -> {b} layers: {errs[a]:.3e} -> {errs[b]:.3e}"
