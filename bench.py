@@ -19,7 +19,9 @@ Qwen2.5-0.5B-architecture model, 4-bit, KV length 512: tokens/s; a step is
 one token, KV rolled back to 512 after each so every step does the same
 work), palettize (the palette compiler: one step palettizes every matrix of
 a Qwen2.5-0.5B-architecture model, fp32 N(0, 0.02) weights resident in HBM,
-k=16, max_iter=50 as compile_to_cimage uses: fp32 params/s).
+k=16, max_iter=50 as compile_to_cimage uses: fp32 params/s), floor (the
+read floor the GEMVs are held to: one launch of the library's streaming-read
+kernel over as many bytes as the hero GEMV reads, rotated the same way).
 """
 from __future__ import annotations
 
@@ -55,6 +57,8 @@ WORKLOADS = {
     "gemm8": ("gemm", 8, 14336, 4096, 2048),  # the cfg5 shape with 8-bit weights (not a BASELINE config)
     "cfg3": ("decode", 4, 0, 0, 1),
     "palettize": ("palettize", 4, 0, 0, 1),
+    # the read floor: one streaming-read launch over the hero's weight bytes
+    "floor": ("floor", 4, 14336, 4096, 1),
 }
 DECODE_KV_LEN = 512
 
@@ -375,49 +379,66 @@ def main() -> int:
 
     log(f"[bench] workload={args.workload} kind={kind} bits={bits} N={N} K={K} batch/M={batch} seed={seed}")
     nmat = 2 if kind == "gateup" else 1
-    tensors = [pe.synth_tensor(N, K, bits, seed=seed + i) for i in range(nmat)]
-    x = pe.synth_x(batch, K, seed=seed)
     wb = weight_bytes(bits, N, K) * nmat
     copies = 1 if kind == "gemm" else max(2, -(-(args.rotate_mb << 20) // wb))
-
     ctx = pe.Context(0)
     dev = torch.device("cuda", 0)
-    weights = [[ctx.upload_tensor(t) for t in tensors] for _ in range(copies)]
-    dx = torch.from_numpy(x.view(np.int16)).to(dev)
-    ny = (batch * N) if kind != "gateup" else N
-    dy = torch.empty(ny, dtype=torch.int16, device=dev)
     stream = torch.cuda.Stream(device=dev)
-    log(f"[bench] {copies} weight copies x {wb / 1e6:.2f} MB = {copies * wb / 1e6:.0f} MB rotated")
 
-    def launch(i: int) -> None:
-        w = weights[i % copies]
-        if kind == "gemv":
-            ctx.gemv_dev(w[0], dx, batch, dy, stream)
-        elif kind == "gateup":
-            ctx.gateup_swiglu_dev(w[0], w[1], dx, dy, stream)
-        else:
-            ctx.gemm_dev(w[0], dx, batch, dy, stream)
+    if kind == "floor":
+        # random bytes, so the kernel's XOR never matches and nothing is written
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bufs = [torch.randint(0, 256, (wb,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
+        sink = torch.zeros(256, dtype=torch.int32, device=dev)
+        log(f"[bench] {copies} buffers x {wb / 1e6:.2f} MB = {copies * wb / 1e6:.0f} MB rotated")
+
+        def launch(i: int) -> None:
+            ctx.stream_read_dev(bufs[i % copies], wb, sink, stream)
+        err = None
+        args.no_cpu = True
+    else:
+        tensors = [pe.synth_tensor(N, K, bits, seed=seed + i) for i in range(nmat)]
+        x = pe.synth_x(batch, K, seed=seed)
+        weights = [[ctx.upload_tensor(t) for t in tensors] for _ in range(copies)]
+        dx = torch.from_numpy(x.view(np.int16)).to(dev)
+        ny = (batch * N) if kind != "gateup" else N
+        dy = torch.empty(ny, dtype=torch.int16, device=dev)
+        log(f"[bench] {copies} weight copies x {wb / 1e6:.2f} MB = {copies * wb / 1e6:.0f} MB rotated")
+
+        def launch(i: int) -> None:
+            w = weights[i % copies]
+            if kind == "gemv":
+                ctx.gemv_dev(w[0], dx, batch, dy, stream)
+            elif kind == "gateup":
+                ctx.gateup_swiglu_dev(w[0], w[1], dx, dy, stream)
+            else:
+                ctx.gemm_dev(w[0], dx, batch, dy, stream)
 
     # correctness guard on a sample before timing (the tests hold the full bar)
     launch(0)
     torch.cuda.synchronize()
-    oracle = importlib.import_module("oracle")
-    yk = dy.cpu().numpy().view(np.uint16)
     if kind == "gemv":
+        oracle = importlib.import_module("oracle")
+        yk = dy.cpu().numpy().view(np.uint16)
         ref = oracle.gemv(x, tensors[0].payload, N, K, bits, threads=min(os.cpu_count() or 1, 16))
         err = max(pe.rel_err(yk.reshape(batch, N)[b], ref[b]) for b in range(batch))
     elif kind == "gateup":
+        oracle = importlib.import_module("oracle")
+        yk = dy.cpu().numpy().view(np.uint16)
         ref = oracle.gateup_swiglu(x[0], tensors[0].payload, tensors[1].payload, N, K, bits,
                                    threads=min(os.cpu_count() or 1, 16))
         err = pe.rel_err(yk, ref)
-    else:
+    elif kind == "gemm":
+        oracle = importlib.import_module("oracle")
+        yk = dy.cpu().numpy().view(np.uint16)
         rows = [0, batch // 2, batch - 1]
         ref = oracle.gemm(np.ascontiguousarray(x[rows]), tensors[0].payload, N, K, bits, threads=8)
         err = max(pe.rel_err(yk.reshape(batch, N)[r], ref[i]) for i, r in enumerate(rows))
-    log(f"[bench] parity check rel_err={err:.3e}")
-    if not err <= 2e-3:
-        log("[bench] PARITY FAILURE")
-        return 1
+    if err is not None:
+        log(f"[bench] parity check rel_err={err:.3e}")
+        if not err <= 2e-3:
+            log("[bench] PARITY FAILURE")
+            return 1
 
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
@@ -475,6 +496,8 @@ def main() -> int:
         unit = "GB/s"
         metric = ("palettized GEMV effective HBM GB/s (% of 8 TB/s peak), 4-bit, batch 1"
                   if args.workload == "hero" else
+                  "streaming-read floor GB/s (one launch over the hero's weight bytes)"
+                  if kind == "floor" else
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": PMC_TRAFFIC.get((args.workload, batch))}
@@ -497,7 +520,7 @@ def main() -> int:
                      "k_gemv_mfma<4,GI64>" if K % 128 == 0 else "k_gemv_lpr<8,1,2> passes (GI64)")
     else:
         gemv_name = f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile"
-    kernel_name = {"gemv": gemv_name,
+    kernel_name = {"floor": "k_stream_read", "gemv": gemv_name,
                    "gateup": "k_gemv_lpr<16,2,1,SwiGLU> (GI64)" if gi else "k_gemv_tile (DUAL gate_up + SwiGLU)",
                    "gemm": ("GEMV passes" if batch <= (48 if bits == 8 else 32) else
                             gemm4 if bits == 4 else
@@ -524,8 +547,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4-index/fp16-LUT, fp32 accumulate" if bits == 4 else "u8-index/fp16-LUT, fp32 accumulate",
-        "data": "synthetic (seeded PCG64: x~N(0,1) fp16, uniform indices, sorted N(0,0.02) fp16 LUTs)",
+        "dtype": ("u8" if kind == "floor" else
+                  "u4-index/fp16-LUT, fp32 accumulate" if bits == 4 else "u8-index/fp16-LUT, fp32 accumulate"),
+        "data": ("synthetic (uniform random bytes)" if kind == "floor" else
+                 "synthetic (seeded PCG64: x~N(0,1) fp16, uniform indices, sorted N(0,0.02) fp16 LUTs)"),
         "config": {"workload": args.workload, "kind": kind, "bits": bits, "N": N, "K": K,
                    ("M" if kind == "gemm" else "batch"): batch, "weight_copies_rotated": copies,
                    "launch": "hip_graph" if graph is not None else "eager", "seed": seed},

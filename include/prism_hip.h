@@ -275,6 +275,13 @@ int prism_hip_model_step(prism_hip_model* m, uint32_t token, int64_t pos, uint16
 int prism_hip_model_step_dev(prism_hip_model* m, uint32_t token, int64_t pos, void* stream);
 const void* prism_hip_model_logits_dev(const prism_hip_model* m);
 
+/* The read floor.  No counterpart in the reference: a measuring stick for the
+ * GEMV kernels above.  Reads each of `bytes` (< 2 GiB) bytes of d_buf once
+ * with the fastest single-launch streaming shape found on MI355X and writes
+ * (almost surely) nothing to d_sink (>= 1 KB of device memory).  Enqueues on
+ * `stream` (NULL: the context stream) and returns. */
+int prism_hip_stream_read_dev(prism_hip_ctx* ctx, const void* d_buf, size_t bytes, void* d_sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,6 +132,11 @@ class Context:
         self.check(self.lib.prism_hip_gate_up_dev(self.h, gate.h, up.h, ptr(d_x), ptr(d_gate), ptr(d_up),
                                                   _stream_handle(stream)))
 
+    def stream_read_dev(self, d_buf, nbytes: int, d_sink, stream=None) -> None:
+        """The read floor: read nbytes of d_buf once (measure_kernels.hpp)."""
+        self.check(self.lib.prism_hip_stream_read_dev(self.h, ptr(d_buf), nbytes, ptr(d_sink),
+                                                      _stream_handle(stream)))
+
     def gemm_dev(self, w: "Weight", d_X, M: int, d_Y, stream=None) -> None:
         self.check(self.lib.prism_hip_gemm_dev(self.h, w.h, ptr(d_X), M, ptr(d_Y), _stream_handle(stream)))
 

@@ -22,6 +22,7 @@
 #include "gemv_tile.hpp"
 #include "gemv_lpr.hpp"
 #include "gemv_mfma.hpp"
+#include "measure_kernels.hpp"
 #include "palette_kernels.hpp"
 #include "step_kernels.hpp"
 
@@ -975,6 +976,21 @@ int prism_hip_lut_embed(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t 
   if ((rc = launch_decode(ctx, w, token, 1, ctx->d_stage, ctx->stream))) return rc;
   HIP_TRY(ctx, hipMemcpyAsync(out, ctx->d_stage, ob, hipMemcpyDeviceToHost, ctx->stream));
   HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+// ---- measurement: the read floor
+int prism_hip_stream_read_dev(prism_hip_ctx* ctx, const void* d_buf, size_t bytes, void* d_sink, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  if (!d_buf || !d_sink) return fail(ctx, PRISM_HIP_ERR_NULL, "buffer or sink is NULL");
+  if (bytes == 0) return PRISM_HIP_OK;
+  if (bytes >= (1ull << 31)) return fail(ctx, PRISM_HIP_ERR_SIZE, "%zu bytes: at most 2 GiB - 1 per call", bytes);
+  DeviceGuard g(ctx->device);
+  const unsigned grid = (unsigned)((bytes + prism::kStreamBytesPerBlock - 1) / prism::kStreamBytesPerBlock);
+  hipLaunchKernelGGL(prism::k_stream_read, dim3(grid), dim3(64), 0, pick_stream(ctx, stream),
+                     reinterpret_cast<const uint8_t*>(d_buf), (uint32_t)bytes, reinterpret_cast<uint32_t*>(d_sink));
+  HIP_TRY(ctx, hipGetLastError());
   ctx->err.clear();
   return PRISM_HIP_OK;
 }
