@@ -143,6 +143,16 @@ int prism_hip_gate_up_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate, cons
 int prism_hip_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t* X, uint32_t M, uint16_t* Y);
 int prism_hip_gemm_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
                        void* stream);
+/* prism_hip_gemm_dev without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same kernels and results as prism_hip_gemm_dev; the split-K partials live
+ * in a static 64 MiB array on each GPU instead of the context's pool, and a
+ * call whose partials would exceed it returns PRISM_HIP_ERR_SIZE (none does
+ * on a 256-CU MI355X).  All calls on one GPU share that array: calls that
+ * overlap on one GPU (other streams, other contexts) race. */
+int prism_hip_gemm_dev_noalloc(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M,
+                               void* d_Y, void* stream);
 
 /* ---- LUT decode ---------------------------------------------------------- */
 

@@ -65,6 +65,7 @@ SIGNATURES = {
     "prism_hip_gate_up_dev": (_c.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "prism_hip_gemm": (_c.c_int, [_vp, _vp, _vp, _c.c_uint32, _vp]),
     "prism_hip_gemm_dev": (_c.c_int, [_vp, _vp, _vp, _c.c_uint32, _vp, _vp]),
+    "prism_hip_gemm_dev_noalloc": (_c.c_int, [_vp, _vp, _vp, _c.c_uint32, _vp, _vp]),
     "prism_hip_lut_embed": (_c.c_int, [_vp, _vp, _c.c_uint32, _vp]),
     "prism_hip_decode_rows_dev": (_c.c_int, [_vp, _vp, _c.c_uint32, _c.c_uint32, _vp, _vp]),
     "prism_hip_palettize_bytes": (_c.c_size_t, [_c.c_uint32, _c.c_uint32]),

@@ -140,6 +140,11 @@ class Context:
     def gemm_dev(self, w: "Weight", d_X, M: int, d_Y, stream=None) -> None:
         self.check(self.lib.prism_hip_gemm_dev(self.h, w.h, ptr(d_X), M, ptr(d_Y), _stream_handle(stream)))
 
+    def gemm_dev_noalloc(self, w: "Weight", d_X, M: int, d_Y, stream=None) -> None:
+        """gemm_dev with its split-K partials in the library's static per-GPU
+        scratch: allocates nothing; overlapping calls on one GPU race."""
+        self.check(self.lib.prism_hip_gemm_dev_noalloc(self.h, w.h, ptr(d_X), M, ptr(d_Y), _stream_handle(stream)))
+
     def decode_rows_dev(self, w: "Weight", row0: int, nrows: int, d_out, stream=None) -> None:
         self.check(self.lib.prism_hip_decode_rows_dev(self.h, w.h, row0, nrows, ptr(d_out),
                                                       _stream_handle(stream)))

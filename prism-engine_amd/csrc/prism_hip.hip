@@ -13,6 +13,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
@@ -39,6 +40,8 @@ struct prism_hip_ctx {
   // created on first use; it keeps what it has allocated, so a call after
   // the first reuses memory instead of allocating.
   hipMemPool_t pool = nullptr;
+  // This device's address of the static split-K scratch (set at create).
+  float* scratch = nullptr;
   std::string err;
   // Weights uploaded through this context; destroying the context orphans
   // them (w->ctx = nullptr) so a later prism_hip_weight_free stays valid.
@@ -66,9 +69,41 @@ struct prism_hip_weight {
   const uint8_t* idx() const { return gi64 ? d : d + (size_t)dim_m * (2u << bits); }
 };
 
+// Split-K partials of prism_hip_gemm_dev_noalloc, the GEMM entry point that
+// allocates nothing: one array on each GPU, held until the process ends.
+// 64 MiB bounds every split the GEMM dispatch makes on a 256-CU MI355X (at
+// most one 256 x 256 fp32 partial tile per CU).  In host code `scratch` is a
+// host-side stand-in, never a device address: device_scratch() looks up each
+// device's copy once, with that device current, and only that address is
+// passed to kernels.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
 namespace {
 
 thread_local std::string g_create_err;
+
+// This device's address of `scratch` (the device is current).
+hipError_t device_scratch(int device, float** out) {
+  static std::mutex mu;
+  static float* addr[64] = {};
+  if (device < 0 || device >= 64) {
+    g_create_err = "device index out of range";
+    return hipErrorInvalidDevice;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) {
+      g_create_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return e;
+    }
+    addr[device] = static_cast<float*>(p);
+  }
+  *out = addr[device];
+  return hipSuccess;
+}
 
 int fail(prism_hip_ctx* ctx, int code, const char* fmt, ...) {
   char buf[512];
@@ -486,8 +521,11 @@ int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_w
 // the K steps are cut into splits of kps steps (every split keeps at least
 // one), the blocks write fp32 partials to a buffer from the context's
 // stream-ordered pool, and k_gemm_split_sum adds them in split order.
+// With `fixed` non-NULL the partials go there instead (at most
+// kScratchBytes; nothing is allocated or freed).
 int launch_gemm_blocks(prism_hip_ctx* ctx, const void* fn, uint32_t tiles, uint32_t nsteps, uint32_t nsplit,
-                       const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y, hipStream_t st) {
+                       const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y, hipStream_t st,
+                       float* fixed) {
   const uint8_t* lut = w->lut();
   const uint8_t* idx = w->idx();
   const uint16_t* X = reinterpret_cast<const uint16_t*>(d_X);
@@ -499,9 +537,17 @@ int launch_gemm_blocks(prism_hip_ctx* ctx, const void* fn, uint32_t tiles, uint3
   if (split) {
     kps = (nsteps + nsplit - 1) / nsplit;
     ns = (nsteps + kps - 1) / kps;
-    int rc = ensure_pool(ctx);
-    if (rc) return rc;
-    HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), (size_t)ns * M * N * 4, ctx->pool, st));
+    const size_t pbytes = (size_t)ns * M * N * 4;
+    if (fixed) {
+      if (pbytes > kScratchBytes)
+        return fail(ctx, PRISM_HIP_ERR_SIZE, "split-K partials of %zu bytes exceed the %zu-byte static scratch",
+                    pbytes, kScratchBytes);
+      P = fixed;
+    } else {
+      int rc = ensure_pool(ctx);
+      if (rc) return rc;
+      HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), pbytes, ctx->pool, st));
+    }
   }
   void* args[] = {&lut, &idx, &X, &Y, &M, &N, &K, &P, &kps};
   hipError_t e = hipLaunchKernel(fn, dim3(tiles, ns), dim3(256), args, 0, st);
@@ -510,7 +556,7 @@ int launch_gemm_blocks(prism_hip_ctx* ctx, const void* fn, uint32_t tiles, uint3
     hipLaunchKernelGGL(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y, mn, ns);
     e = hipGetLastError();
   }
-  if (split) {
+  if (split && !fixed) {
     const hipError_t f = hipFreeAsync(P, st);
     if (e == hipSuccess) e = f;
   }
@@ -519,7 +565,7 @@ int launch_gemm_blocks(prism_hip_ctx* ctx, const void* fn, uint32_t tiles, uint3
 }
 
 int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M, void* d_Y,
-                hipStream_t st) {
+                hipStream_t st, float* fixed = nullptr) {
   const uint32_t N = w->dim_m, K = w->dim_n, bits = w->bits;
   const bool fast = (K % prism::GEMM_BK == 0) && (reinterpret_cast<uintptr_t>(d_X) % 16 == 0);
   // Up to 32 rows of X (48 for 8-bit weights): GEMV passes of up to 16
@@ -572,7 +618,7 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
     else
       fn = mi == 2 ? PRISM_W4(2, false) : mi == 4 ? PRISM_W4(4, false) : PRISM_W4(8, false);
 #undef PRISM_W4
-    return launch_gemm_blocks(ctx, fn, tiles4, nsteps, nsplit, w, d_X, M, d_Y, st);
+    return launch_gemm_blocks(ctx, fn, tiles4, nsteps, nsplit, w, d_X, M, d_Y, st, fixed);
   }
   // 8-bit, K % 64 == 0, more than 256 rows: 256 x 128 blocks over a 64-wide
   // K step (k_gemm8).  MI355X, 14336x4096: M = 384 / 512 / 2048 take 118 /
@@ -595,7 +641,7 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
       const uint32_t nsplit8 = M <= 256 ? sk8 : 1;
       const void* fn = nsplit8 > 1 ? reinterpret_cast<const void*>(&prism::k_gemm8<true>)
                                    : reinterpret_cast<const void*>(&prism::k_gemm8<false>);
-      return launch_gemm_blocks(ctx, fn, tiles8, nsteps, nsplit8, w, d_X, M, d_Y, st);
+      return launch_gemm_blocks(ctx, fn, tiles8, nsteps, nsplit8, w, d_X, M, d_Y, st, fixed);
     }
   }
   // GI64 weights (K % 64 == 0, below 2 GiB) always take k_gemm_w4 above.
@@ -688,8 +734,11 @@ prism_hip_ctx* prism_hip_ctx_create(int device) {
     g_create_err = std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950";
     return nullptr;
   }
+  float* scratch = nullptr;
+  if (device_scratch(device, &scratch) != hipSuccess) return nullptr;
   auto* ctx = new prism_hip_ctx;
   ctx->device = device;
+  ctx->scratch = scratch;
   ctx->num_cu = prop.multiProcessorCount;
   ctx->lds_max = prop.sharedMemPerBlock;
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
@@ -922,6 +971,19 @@ int prism_hip_gemm_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void
   if (M == 0) return PRISM_HIP_OK;
   DeviceGuard g(ctx->device);
   rc = launch_gemm(ctx, w, d_X, M, d_Y, pick_stream(ctx, stream));
+  if (rc == PRISM_HIP_OK) ctx->err.clear();
+  return rc;
+}
+
+int prism_hip_gemm_dev_noalloc(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, uint32_t M,
+                               void* d_Y, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  int rc = check_weight(ctx, w);
+  if (rc) return rc;
+  if (!d_X || !d_Y) return fail(ctx, PRISM_HIP_ERR_NULL, "X or Y is NULL");
+  if (M == 0) return PRISM_HIP_OK;
+  DeviceGuard g(ctx->device);
+  rc = launch_gemm(ctx, w, d_X, M, d_Y, pick_stream(ctx, stream), ctx->scratch);
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;
 }
