@@ -495,7 +495,7 @@ def main() -> int:
         value = wb / (ms_step * 1e-3) / 1e9
         unit = "GB/s"
         metric = ("palettized GEMV effective HBM GB/s (% of 8 TB/s peak), 4-bit, batch 1"
-                  if args.workload == "hero" else
+                  if args.workload == "hero" and batch == 1 else
                   "streaming-read floor GB/s (one launch over the hero's weight bytes)"
                   if kind == "floor" else
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")

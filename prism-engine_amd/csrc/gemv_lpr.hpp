@@ -32,11 +32,12 @@
 //    half its LDS cycles to conflicts).  One v_perm builds the address
 //    (lane*4 in byte 0, the index byte in byte 1) and one ds_read_b32 reads
 //    the pair: per element one VALU op and half an LDS read, plus the v_dot2.
-//  * Loads: the LUTs, the first P chunks per wave and the first x block go
-//    out first; after the table build each wave keeps P chunk loads in
-//    flight, so the index stream is requested at the rate the lookups
-//    consume it (with every chunk requested up front, the waves whose
-//    chunks return last decode all of theirs at the end).  Chunk loads are
+//  * Loads: the LUTs (two 16-byte loads per lane), the first P chunks per
+//    wave and the first x block go out first; after the table build each
+//    wave keeps P chunk loads in flight, so the index stream is requested
+//    at the rate the lookups consume it (with every chunk requested up
+//    front, the waves whose chunks return last decode all of theirs at the
+//    end; with 8 in flight the hero shape also ran slower).  Chunk loads are
 //    unconditional (past the wave's range they read zeros through the range
 //    check), so the compiler's wait counts stay exact instead of falling
 //    back to waiting for every load.
@@ -99,18 +100,18 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   const uint32_t c0 = (w * NC) / S, nch = ((w + 1) * NC) / S - c0;
   const uint32_t gbase = g * (uint32_t)gi64_group_bytes(K);
 
-  // ---- the LUTs of the lane's row: 8 dwords and its LO low-nibble entries
-  // (entry e = w + S i: low nibble w + S (i % LO), high nibble i / LO).
-  // Lanes past N read the zero LUT slots of the last group's padding rows.
-  uint32_t L[NM][8], hv[NM][LO];
+  // ---- the LUT of the lane's row: 8 dwords, two 16-byte loads and nothing
+  // else (the table build waits for them: a separate load of the low-nibble
+  // entries a wave needs cost 0.4 us on the hero shape; they are picked out
+  // of these registers below).  Lanes past N read the zero LUT slots of the
+  // last group's padding rows.
+  uint32_t L[NM][8];
 #pragma unroll
   for (int m = 0; m < NM; m++) {
     const uint8_t* lb = (m == 0 ? a.w : a.w2) + gbase + lane * 32u;
     const uint4 l0 = reinterpret_cast<const uint4*>(lb)[0], l1 = reinterpret_cast<const uint4*>(lb)[1];
     L[m][0] = l0.x; L[m][1] = l0.y; L[m][2] = l0.z; L[m][3] = l0.w;
     L[m][4] = l1.x; L[m][5] = l1.y; L[m][6] = l1.z; L[m][7] = l1.w;
-#pragma unroll
-    for (int j = 0; j < LO; j++) hv[m][j] = reinterpret_cast<const uint16_t*>(lb)[w + S * j];
   }
 
   // ---- index chunks: a ring of P per matrix.  Every load is issued
@@ -149,7 +150,20 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   };
   ldx(0);
 
-  // ---- bank-private pair tables
+  // ---- bank-private pair tables.  The wave builds entries e = w + S i:
+  // low nibble w + S (i % LO), high nibble i / LO.  Its LO low-nibble fp16
+  // values are LUT entries w + S j, selected from L with the wave-uniform w.
+  uint32_t hv[NM][LO];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int j = 0; j < LO; j++) {
+      const uint32_t e = w + S * j;
+      uint32_t d = L[m][0];
+#pragma unroll
+      for (int q = 1; q < 8; q++) d = (e >> 1) == (uint32_t)q ? L[m][q] : d;
+      hv[m][j] = (e & 1) ? (d >> 16) : (d & 0xFFFFu);
+    }
 #pragma unroll
   for (int m = 0; m < NM; m++)
 #pragma unroll
