@@ -21,7 +21,9 @@ work), palettize (the palette compiler: one step palettizes every matrix of
 a Qwen2.5-0.5B-architecture model, fp32 N(0, 0.02) weights resident in HBM,
 k=16, max_iter=50 as compile_to_cimage uses: fp32 params/s), floor (the
 read floor the GEMVs are held to: one launch of the library's streaming-read
-kernel over as many bytes as the hero GEMV reads, rotated the same way).
+kernel over as many bytes as the hero GEMV reads, rotated the same way),
+load (a step is one load_cimage of a Qwen2.5-0.5B-sized 4-bit .cimage: mmap,
+every tensor through the pinned staging ring, one wait; GB/s of payload).
 """
 from __future__ import annotations
 
@@ -59,7 +61,10 @@ WORKLOADS = {
     "palettize": ("palettize", 4, 0, 0, 1),
     # the read floor: one streaming-read launch over the hero's weight bytes
     "floor": ("floor", 4, 14336, 4096, 1),
+    # .cimage -> device: load_cimage of a Qwen2.5-0.5B-sized file
+    "load": ("load", 4, 0, 0, 1),
 }
+PCIE_PEAK_GBS = 63.0  # PCIe 5.0 x16, one direction
 DECODE_KV_LEN = 512
 
 
@@ -90,6 +95,25 @@ def weight_bytes(bits: int, N: int, K: int) -> int:
     return N * (2 << bits) + N * (K // 2 if bits == 4 else K)
 
 
+class _pinned_core:
+    """Run the enclosed single-thread baseline on one host core."""
+
+    def __enter__(self):
+        self.old = None
+        self.core = None
+        try:
+            self.old = os.sched_getaffinity(0)
+            self.core = min(self.old)
+            os.sched_setaffinity(0, {self.core})
+        except (AttributeError, OSError):
+            self.old = None
+        return self
+
+    def __exit__(self, *a):
+        if self.old is not None:
+            os.sched_setaffinity(0, self.old)
+
+
 def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
     """The oracle (a C restatement of lut_gemv_cpu, single thread like the
     reference) timed on this host on a bounded sample of the workload."""
@@ -98,15 +122,16 @@ def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
     t0 = tensors[0]
     if kind == "gemm":
         # M independent GEMV rows; sample rows until the budget is spent
-        rows, t_start = 0, time.perf_counter()
-        while time.perf_counter() - t_start < budget_s and rows < batch:
-            oracle.gemm(np.ascontiguousarray(x[rows:rows + 1]), t0.payload, N, K, bits, threads=1)
-            rows += 1
-        dt = time.perf_counter() - t_start
+        with _pinned_core() as pin:
+            rows, t_start = 0, time.perf_counter()
+            while time.perf_counter() - t_start < budget_s and rows < batch:
+                oracle.gemm(np.ascontiguousarray(x[rows:rows + 1]), t0.payload, N, K, bits, threads=1)
+                rows += 1
+            dt = time.perf_counter() - t_start
         flops = 2.0 * rows * N * K
         return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
                 "sample": f"{rows} of {batch} GEMM rows (oracle, 1 thread) in {dt:.1f} s",
-                "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+                "pinned_core": pin.core, "cpu": cpu_model(), "host_cpus": os.cpu_count()}
 
     def one():
         if kind == "gateup":
@@ -114,14 +139,15 @@ def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
         else:
             oracle.gemv(x, t0.payload, N, K, bits, threads=1)
 
-    t_start = time.perf_counter()
-    one()
-    t1 = time.perf_counter() - t_start
-    n = max(1, min(1000, int(budget_s / max(t1, 1e-6))))
-    t_start = time.perf_counter()
-    for _ in range(n):
+    with _pinned_core() as pin:
+        t_start = time.perf_counter()
         one()
-    dt = (time.perf_counter() - t_start) / n
+        t1 = time.perf_counter() - t_start
+        n = max(1, min(1000, int(budget_s / max(t1, 1e-6))))
+        t_start = time.perf_counter()
+        for _ in range(n):
+            one()
+        dt = (time.perf_counter() - t_start) / n
     nbytes = weight_bytes(bits, N, K) * (2 if kind == "gateup" else 1)
     # informational: the row-parallel variant on every host core (bit-identical)
     threads = min(os.cpu_count() or 1, 16)
@@ -133,7 +159,7 @@ def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
     dt_mt = time.perf_counter() - ts
     return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{n + 1} full {kind} calls of the workload (oracle, 1 thread), {dt * 1e3:.2f} ms each",
-            "all_core_value": round(nbytes / dt_mt / 1e9, 4), "all_core_threads": threads,
+            "pinned_core": pin.core, "all_core_value": round(nbytes / dt_mt / 1e9, 4), "all_core_threads": threads,
             "cpu": cpu_model(), "host_cpus": os.cpu_count()}
 
 
@@ -203,15 +229,16 @@ def run_decode(args, pe, seed) -> int:
         for l, (k, v) in enumerate(kvs):
             for t in range(L0):
                 kv_c.append(l, k[t], v[t])
-        n, t0 = 0, time.perf_counter()
-        while n < 1 or time.perf_counter() - t0 < 8.0:
-            kv_c.len[:] = L0
-            oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv_c, 42 + n, L0, threads=1)
-            n += 1
-        dt = (time.perf_counter() - t0) / n
+        with _pinned_core() as pin:
+            n, t0 = 0, time.perf_counter()
+            while n < 1 or time.perf_counter() - t0 < 8.0:
+                kv_c.len[:] = L0
+                oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv_c, 42 + n, L0, threads=1)
+                n += 1
+            dt = (time.perf_counter() - t0) / n
         cpu = {"value": round(1.0 / dt, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
                "sample": f"{n} decode steps at KV {L0} (oracle, 1 thread), {dt * 1e3:.0f} ms each",
-               "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+               "pinned_core": pin.core, "cpu": cpu_model(), "host_cpus": os.cpu_count()}
         log(f"[bench] cpu baseline {cpu['value']} tokens/s")
 
     rec = {
@@ -299,16 +326,17 @@ def run_palettize(args, pe, seed) -> int:
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
         host = [(w[:max(1, w.shape[0] // 8)].cpu().numpy()) for w in ws]
-        t0 = time.perf_counter()
-        done = 0
-        for h in host:
-            oracle.palettize_payload(h, 16, 50, threads=1)
-            done += h.size
-        dt = time.perf_counter() - t0
+        with _pinned_core() as pin:
+            t0 = time.perf_counter()
+            done = 0
+            for h in host:
+                oracle.palettize_payload(h, 16, 50, threads=1)
+                done += h.size
+            dt = time.perf_counter() - t0
         cpu = {"value": round(done / dt / 1e6, 4), "unit": "Mparams/s", "cores": 1, "kind": "port",
                "sample": f"first 1/8 of the rows of every matrix ({done / 1e6:.1f} M params, oracle, 1 thread), "
                          f"{dt:.1f} s",
-               "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+               "pinned_core": pin.core, "cpu": cpu_model(), "host_cpus": os.cpu_count()}
         log(f"[bench] cpu baseline {cpu['value']} Mparams/s")
 
     value = params / (ms_step * 1e-3) / 1e6
@@ -338,6 +366,101 @@ def run_palettize(args, pe, seed) -> int:
     return 0
 
 
+def run_load(args, pe, seed) -> int:
+    """load_cimage timed end to end: mmap of the file, every palettized
+    tensor through the context's pinned staging ring (GI64 regrouping on
+    the device where it applies), one wait.  The file is a Qwen2.5-0.5B-
+    sized 4-bit .cimage with random payload bytes, written to the host's
+    temporary directory first (so it is read from the page cache)."""
+    import tempfile
+
+    import torch
+    cfg = pe.Qwen2Config()
+    names = pe.tensor_names(cfg)
+    shapes = cfg.shapes()
+    tensors = [(names["embed"], cfg.vocab, cfg.hidden)]
+    for l in range(cfg.n_layers):
+        for role, key in names["layers"][l].items():
+            tensors.append((key, shapes[role][0], shapes[role][1]))
+    rng = np.random.Generator(np.random.PCG64(seed))
+    fd, path = tempfile.mkstemp(suffix=".cimage")
+    os.close(fd)
+    total = 0
+    try:
+        w = pe.CImageWriter(path)
+        for key, m, n in tensors:
+            nb = m * 32 + m * n // 2
+            w.append_palettized(key, rng.integers(0, 256, size=nb, dtype=np.uint8), m, n, 4)
+            total += nb
+        w.finalize()
+        fsize = os.path.getsize(path)
+        log(f"[bench] workload=load: {len(tensors)} tensors, {total / 1e6:.1f} MB of payload, file {fsize / 1e6:.1f} MB")
+
+        def one() -> float:
+            t0 = time.perf_counter()
+            b = pe.load_cimage(path)
+            dt = time.perf_counter() - t0
+            n = len(b)
+            b.close()
+            if n != len(tensors):
+                raise RuntimeError(f"loaded {n} of {len(tensors)} tensors")
+            return dt
+
+        for _ in range(args.warmup):
+            one()
+        times = [one() for _ in range(args.steps)]
+        dt = float(np.median(times))
+        value = total / dt / 1e9
+        log(f"[bench] {args.steps} loads: median {dt * 1e3:.1f} ms ({value:.2f} GB/s), "
+            f"min {min(times) * 1e3:.1f} ms")
+
+        # context: each payload copied from the mapping as a pageable torch
+        # tensor with a wait per tensor (the per-tensor synchronous pattern)
+        r = pe.CImageReader(path)
+        dev = torch.device("cuda", 0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for key, m, n in tensors:
+            torch.from_numpy(np.asarray(r.payload(key))).to(dev)
+            torch.cuda.synchronize()
+        pageable = total / (time.perf_counter() - t0) / 1e9
+        r.close()
+
+        cpu = None
+        if not args.no_cpu:
+            # the reference's host side: fs::read of the whole file, then a
+            # copy of each payload (MetalBackend::new's newBufferWithBytes)
+            with _pinned_core() as pin:
+                t0 = time.perf_counter()
+                with open(path, "rb") as f:
+                    data = f.read()
+                rr = pe.CImageReader(path)
+                for key, m, n in tensors:
+                    rec = rr.tensors[key]
+                    bytearray(data[rec["offset"]:rec["offset"] + rec["size"]])
+                rr.close()
+                dc = time.perf_counter() - t0
+            cpu = {"value": round(total / dc / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                   "sample": f"one read of the {fsize / 1e6:.0f} MB file plus a copy of each payload, {dc * 1e3:.0f} ms",
+                   "pinned_core": pin.core, "cpu": cpu_model(), "host_cpus": os.cpu_count()}
+    finally:
+        os.unlink(path)
+    rec = {
+        "metric": "load_cimage GB/s (.cimage mmap -> device, Qwen2.5-0.5B size, 4-bit)",
+        "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic (random payload bytes, Qwen2.5-0.5B tensor shapes)",
+        "config": {"workload": "load", "kind": "load", "tensors": len(tensors), "payload_bytes": total,
+                   "file_bytes": fsize, "seed": seed},
+        "roofline": {"bound": "pcie", "achieved": round(value, 3), "peak": PCIE_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / PCIE_PEAK_GBS, 4), "traffic": None, "kernel": "hipMemcpyAsync H2D"},
+        "pageable_per_tensor_GBps": round(pageable, 3),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,9 +478,9 @@ def main() -> int:
     args = ap.parse_args()
     # a palettize step compiles a whole model (about 0.1 s)
     if args.steps is None:
-        args.steps = 10 if args.workload == "palettize" else 2000
+        args.steps = 10 if args.workload in ("palettize", "load") else 2000
     if args.warmup is None:
-        args.warmup = 2 if args.workload == "palettize" else 50
+        args.warmup = 2 if args.workload in ("palettize", "load") else 50
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -373,6 +496,8 @@ def main() -> int:
         return run_decode(args, pe, pe.SEEDS.get(args.workload, 1003))
     if kind == "palettize":
         return run_palettize(args, pe, pe.SEEDS.get(args.workload, 1006))
+    if kind == "load":
+        return run_load(args, pe, pe.SEEDS.get(args.workload, 1007))
     if args.batch is not None and kind in ("gemv", "gemm"):
         batch = args.batch  # batch vectors, or the GEMM's rows of X
     seed = pe.SEEDS.get(args.workload, 1000)

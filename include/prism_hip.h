@@ -83,6 +83,16 @@ const char* prism_hip_version(void);
  * NULL on failure (reason in prism_hip_last_error(ctx)). */
 prism_hip_weight* prism_hip_weight_upload(prism_hip_ctx* ctx, const uint8_t* payload, size_t bytes,
                                           uint32_t dim_m, uint32_t dim_n, uint32_t bits, uint32_t layout);
+/* prism_hip_weight_upload without the final wait, for uploading a whole
+ * model (MetalBackend::new's loop, engine_impl.rs:124-133) with one wait at
+ * the end.  The payload is consumed (copied into the context's pinned
+ * staging ring) before the call returns; the device copy completes in order
+ * on the context stream, so every later call on this context sees it.  Call
+ * prism_hip_ctx_synchronize before using the weight on another stream. */
+prism_hip_weight* prism_hip_weight_upload_async(prism_hip_ctx* ctx, const uint8_t* payload, size_t bytes,
+                                                uint32_t dim_m, uint32_t dim_n, uint32_t bits, uint32_t layout);
+/* Wait for everything enqueued on the context stream (uploads included). */
+int prism_hip_ctx_synchronize(prism_hip_ctx* ctx);
 /* Same, from a payload already in device memory (copied device-to-device). */
 prism_hip_weight* prism_hip_weight_upload_dev(prism_hip_ctx* ctx, const void* d_payload, size_t bytes,
                                               uint32_t dim_m, uint32_t dim_n, uint32_t bits, uint32_t layout);
@@ -220,6 +230,9 @@ int prism_hip_backend_embed(prism_hip_backend* b, const char* key, uint32_t toke
                             size_t out_len);
 /* Number of registered tensors. */
 size_t prism_hip_backend_len(const prism_hip_backend* b);
+/* add_tensor uploads asynchronously on the backend's own stream (its other
+ * calls are ordered after them); this waits for every upload to finish. */
+int prism_hip_backend_synchronize(prism_hip_backend* b);
 
 /* ---- GPU-resident decode step ----------------------------------------------
  * Replaces PrismEngine::step (src/lut/engine_impl.rs:1076-1405) for the

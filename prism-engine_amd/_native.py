@@ -55,6 +55,9 @@ SIGNATURES = {
     "prism_hip_weight_upload": (_vp, [_vp, _vp, _c.c_size_t, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_uint32]),
     "prism_hip_weight_upload_dev": (_vp, [_vp, _vp, _c.c_size_t, _c.c_uint32, _c.c_uint32, _c.c_uint32,
                                           _c.c_uint32]),
+    "prism_hip_weight_upload_async": (_vp, [_vp, _vp, _c.c_size_t, _c.c_uint32, _c.c_uint32, _c.c_uint32,
+                                            _c.c_uint32]),
+    "prism_hip_ctx_synchronize": (_c.c_int, [_vp]),
     "prism_hip_weight_free": (None, [_vp]),
     "prism_hip_weight_info": (_c.c_int, [_vp, _u32p, _u32p, _u32p, _szp]),
     "prism_hip_gemv": (_c.c_int, [_vp, _vp, _vp, _c.c_uint32, _vp]),
@@ -84,6 +87,7 @@ SIGNATURES = {
     "prism_hip_backend_gemm": (_c.c_int, [_vp, _c.c_char_p, _vp, _c.c_uint32, _vp]),
     "prism_hip_backend_embed": (_c.c_int, [_vp, _c.c_char_p, _c.c_uint32, _vp, _c.c_size_t]),
     "prism_hip_backend_len": (_c.c_size_t, [_vp]),
+    "prism_hip_backend_synchronize": (_c.c_int, [_vp]),
     "prism_hip_model_create": (_vp, [_vp, _cfgp]),
     "prism_hip_model_free": (None, [_vp]),
     "prism_hip_model_set_embedding": (_c.c_int, [_vp, _vp]),

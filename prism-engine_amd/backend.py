@@ -70,6 +70,20 @@ class Context:
             raise PrismHipError(_native.ERR_SHAPE, self.error())
         return Weight(self, h, dim_m, dim_n, bits, payload.size)
 
+    def upload_async(self, payload: np.ndarray, dim_m: int, dim_n: int, bits: int) -> "Weight":
+        """upload() without the final wait (the payload is consumed before
+        return; the device copy is ordered on the context stream).  Call
+        synchronize() before using the weight on another stream."""
+        payload = np.ascontiguousarray(payload, dtype=np.uint8)
+        h = self.lib.prism_hip_weight_upload_async(self.h, payload.ctypes.data, payload.size, dim_m, dim_n, bits,
+                                                   _native.LAYOUT_SPLIT_BLOCK)
+        if not h:
+            raise PrismHipError(_native.ERR_SHAPE, self.error())
+        return Weight(self, h, dim_m, dim_n, bits, payload.size)
+
+    def synchronize(self) -> None:
+        self.check(self.lib.prism_hip_ctx_synchronize(self.h))
+
     def upload_tensor(self, t: PalettizedTensor) -> "Weight":
         return self.upload(t.payload, t.dim_m, t.dim_n, t.bits)
 
@@ -320,6 +334,7 @@ class HipBackend:
         items = tensors.values() if isinstance(tensors, dict) else tensors
         for t in items:
             b.add_tensor(t.key, t.payload, t.dim_m, t.dim_n, t.bits)
+        b.synchronize()
         return b
 
     def _check(self, rc: int) -> None:
@@ -328,6 +343,10 @@ class HipBackend:
 
     def __len__(self) -> int:
         return int(self.lib.prism_hip_backend_len(self.h))
+
+    def synchronize(self) -> None:
+        """Wait for every add_tensor upload (they are asynchronous)."""
+        self._check(self.lib.prism_hip_backend_synchronize(self.h))
 
     def add_tensor(self, key: str, payload, dim_m: int, dim_n: int, bits: int = 4) -> None:
         payload = np.ascontiguousarray(payload, dtype=np.uint8)
@@ -378,15 +397,18 @@ class HipBackend:
             pass
 
 
-def load_cimage(path: str, device: int = 0) -> HipBackend:
+def load_cimage(path: str, device: int = 0, populate: bool = True) -> HipBackend:
     """Upload every palettized tensor of a `.cimage` file into a HipBackend
     (engine_impl.rs:597-636 + MetalBackend::new's upload, :124-133).  The
-    payloads are memory-mapped, not read whole."""
+    payloads are memory-mapped, not read whole; each goes through the
+    context's pinned staging ring without a wait, and one wait at the end
+    makes them all usable from any stream."""
     from .cimage import CImageReader, bits_of
     b = HipBackend(device)
-    with CImageReader(path) as r:
+    with CImageReader(path, populate=populate) as r:
         for name, rec in r.tensors.items():
             if rec["tensor_type"] not in ("Palettized4Bit", "Palettized8Bit"):
                 continue
             b.add_tensor(name, r.payload(name), rec["dim_m"], rec["dim_n"], bits_of(rec["tensor_type"]))
+        b.synchronize()
     return b

@@ -77,7 +77,9 @@ class CImageReader:
     """Header parser plus zero-copy payload views (cimage.rs:240-303); the
     payloads are memory-mapped instead of read whole (engine_impl.rs:600)."""
 
-    def __init__(self, path: str):
+    def __init__(self, path: str, populate: bool = False):
+        """populate: map every page up front (MAP_POPULATE), for a reader
+        that will touch the whole file, such as a loader."""
         self.path = path
         with open(path, "rb") as f:
             magic = f.read(8)
@@ -87,7 +89,13 @@ class CImageReader:
             self.header = json.loads(f.read(hsize))
         self._f = open(path, "rb")
         size = os.fstat(self._f.fileno()).st_size
-        self._mm = mmap.mmap(self._f.fileno(), 0, access=mmap.ACCESS_READ) if size else None
+        if not size:
+            self._mm = None
+        elif populate and hasattr(mmap, "MAP_POPULATE"):
+            self._mm = mmap.mmap(self._f.fileno(), 0, flags=mmap.MAP_SHARED | mmap.MAP_POPULATE,
+                                 prot=mmap.PROT_READ)
+        else:
+            self._mm = mmap.mmap(self._f.fileno(), 0, access=mmap.ACCESS_READ)
 
     @property
     def tensors(self) -> dict:

@@ -34,8 +34,10 @@ const prism_hip_weight* HipBackend::find(const std::string& key) const {
 
 std::string HipBackend::add_tensor(const std::string& key, const uint8_t* payload, size_t bytes, uint32_t dim_m,
                                    uint32_t dim_n, uint32_t bits) {
+  // asynchronous: every other call of the backend runs on the same stream,
+  // after the copy; synchronize() waits for all of them
   prism_hip_weight* w =
-      prism_hip_weight_upload(ctx_, payload, bytes, dim_m, dim_n, bits, PRISM_HIP_LAYOUT_SPLIT_BLOCK);
+      prism_hip_weight_upload_async(ctx_, payload, bytes, dim_m, dim_n, bits, PRISM_HIP_LAYOUT_SPLIT_BLOCK);
   if (!w) return key + ": " + prism_hip_last_error(ctx_);
   auto it = weights_.find(key);
   if (it != weights_.end()) {
@@ -45,6 +47,11 @@ std::string HipBackend::add_tensor(const std::string& key, const uint8_t* payloa
     weights_.emplace(key, w);
   }
   return "";
+}
+
+std::string HipBackend::synchronize() {
+  const int rc = prism_hip_ctx_synchronize(ctx_);
+  return rc == PRISM_HIP_OK ? "" : hip_err(rc);
 }
 
 std::string HipBackend::gemv(const std::string& key, const uint16_t* inp, size_t inp_len, uint16_t* out,
@@ -183,5 +190,11 @@ int prism_hip_backend_embed(prism_hip_backend* b, const char* key, uint32_t toke
 }
 
 size_t prism_hip_backend_len(const prism_hip_backend* b) { return b ? b->impl->len() : 0; }
+
+int prism_hip_backend_synchronize(prism_hip_backend* b) {
+  if (!b) return PRISM_HIP_ERR_NULL;
+  const std::string e = b->impl->synchronize();
+  return finish(b, e, e.empty() ? PRISM_HIP_OK : PRISM_HIP_ERR_DEVICE);
+}
 
 }  // extern "C"

@@ -7,8 +7,9 @@
 //   MetalBackend::fused_gate_up(g, u, x, y)  -> HipBackend::fused_gate_up
 // Errors are the reference's `Result<(), String>`: an empty string is Ok,
 // anything else is the Err text ("miss <key>" for an unknown tensor, as at
-// engine_impl.rs:156-159).  Every method is synchronous on the backend's
-// stream, like the reference's commit + wait_until_completed.
+// engine_impl.rs:156-159).  Every compute method is synchronous on the
+// backend's stream, like the reference's commit + wait_until_completed;
+// add_tensor only enqueues its device copy (synchronize() waits for them).
 // Unlike the reference's caller (PrismEngine::gemv, engine_impl.rs:1489-1504)
 // nothing here falls back to the CPU: an Err is the caller's to handle.
 #pragma once
@@ -38,6 +39,8 @@ class HipBackend {
                             size_t in_len, uint16_t* output, size_t out_len);
   std::string gemm(const std::string& key, const uint16_t* X, uint32_t M, uint16_t* Y);
   std::string embed(const std::string& key, uint32_t token, uint16_t* out, size_t out_len);
+  // Waits for every add_tensor upload (they are asynchronous on the stream).
+  std::string synchronize();
 
   size_t len() const { return weights_.size(); }
   const prism_hip_weight* find(const std::string& key) const;

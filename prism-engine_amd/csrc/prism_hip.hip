@@ -15,6 +15,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <unordered_set>
 
@@ -42,6 +43,16 @@ struct prism_hip_ctx {
   hipMemPool_t pool = nullptr;
   // This device's address of the static split-K scratch (set at create).
   float* scratch = nullptr;
+  // Host uploads: a ring of pinned staging buffers (created on first use),
+  // each with the event of the last copy out of it, and a device buffer for
+  // split-block payloads on their way to the GI64 layout.
+  static constexpr int kRingSlots = 4;
+  static constexpr size_t kRingSlotBytes = (size_t)16 << 20;
+  void* ring[kRingSlots] = {};
+  hipEvent_t ring_done[kRingSlots] = {};
+  int ring_next = 0;
+  void* d_upload = nullptr;
+  size_t upload_bytes = 0;
   std::string err;
   // Weights uploaded through this context; destroying the context orphans
   // them (w->ctx = nullptr) so a later prism_hip_weight_free stays valid.
@@ -150,6 +161,66 @@ int ensure_stage(prism_hip_ctx* ctx, size_t bytes) {
   while (sz < bytes) sz <<= 1;
   HIP_TRY(ctx, hipMalloc(&ctx->d_stage, sz));
   ctx->stage_bytes = sz;
+  return PRISM_HIP_OK;
+}
+
+int ensure_upload_stage(prism_hip_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->upload_bytes) return PRISM_HIP_OK;
+  if (ctx->d_upload) {
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipFree(ctx->d_upload));
+    ctx->d_upload = nullptr;
+    ctx->upload_bytes = 0;
+  }
+  size_t sz = 1 << 20;
+  while (sz < bytes) sz <<= 1;
+  HIP_TRY(ctx, hipMalloc(&ctx->d_upload, sz));
+  ctx->upload_bytes = sz;
+  return PRISM_HIP_OK;
+}
+
+// memcpy of n bytes, split over up to 4 host threads for large pieces (one
+// thread copies about 10 GB/s out of the page cache; the PCIe link takes
+// several times that).
+void host_copy(void* dst, const void* src, size_t n) {
+  constexpr size_t kPerThread = (size_t)4 << 20;
+  const size_t nt = std::min<size_t>(4, n / kPerThread);
+  if (nt < 2) {
+    std::memcpy(dst, src, n);
+    return;
+  }
+  const size_t part = (n / nt + 4095) & ~(size_t)4095;
+  std::thread th[3];
+  for (size_t t = 1; t < nt; t++) {
+    const size_t o = t * part;
+    const size_t len = o >= n ? 0 : std::min(part, n - o);
+    th[t - 1] = std::thread([=] { std::memcpy(static_cast<char*>(dst) + o, static_cast<const char*>(src) + o, len); });
+  }
+  std::memcpy(dst, src, std::min(part, n));
+  for (size_t t = 1; t < nt; t++) th[t - 1].join();
+}
+
+// Host -> device copy of `bytes` through the pinned ring, in pieces of one
+// slot: each piece waits for the last copy out of its slot, is copied into
+// it on the host, and its device copy is enqueued on the context stream.
+// `src` is consumed before the call returns; the device copies complete in
+// stream order.
+int stage_h2d(prism_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx->ring[0]) {
+    for (int i = 0; i < prism_hip_ctx::kRingSlots; i++) {
+      HIP_TRY(ctx, hipHostMalloc(&ctx->ring[i], prism_hip_ctx::kRingSlotBytes, hipHostMallocDefault));
+      HIP_TRY(ctx, hipEventCreateWithFlags(&ctx->ring_done[i], hipEventDisableTiming));
+    }
+  }
+  for (size_t off = 0; off < bytes; off += prism_hip_ctx::kRingSlotBytes) {
+    const size_t n = std::min(prism_hip_ctx::kRingSlotBytes, bytes - off);
+    const int slot = ctx->ring_next;
+    ctx->ring_next = (slot + 1) % prism_hip_ctx::kRingSlots;
+    HIP_TRY(ctx, hipEventSynchronize(ctx->ring_done[slot]));
+    host_copy(ctx->ring[slot], static_cast<const char*>(src) + off, n);
+    HIP_TRY(ctx, hipMemcpyAsync(static_cast<char*>(dst) + off, ctx->ring[slot], n, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(ctx, hipEventRecord(ctx->ring_done[slot], ctx->stream));
+  }
   return PRISM_HIP_OK;
 }
 
@@ -762,6 +833,11 @@ void prism_hip_ctx_destroy(prism_hip_ctx* ctx) {
     (void)hipStreamDestroy(ctx->stream);
   }
   if (ctx->d_stage) (void)hipFree(ctx->d_stage);
+  if (ctx->d_upload) (void)hipFree(ctx->d_upload);
+  for (int i = 0; i < prism_hip_ctx::kRingSlots; i++) {
+    if (ctx->ring[i]) (void)hipHostFree(ctx->ring[i]);
+    if (ctx->ring_done[i]) (void)hipEventDestroy(ctx->ring_done[i]);
+  }
   if (ctx->pool) {
     (void)hipDeviceSynchronize();  // scratch freed on other streams
     (void)hipMemPoolDestroy(ctx->pool);
@@ -773,8 +849,12 @@ const char* prism_hip_last_error(const prism_hip_ctx* ctx) {
   return ctx ? ctx->err.c_str() : g_create_err.c_str();
 }
 
+// Host payloads go through the pinned ring (stage_h2d); device payloads
+// are copied device-to-device.  GI64 weights are regrouped on the device
+// from a split-block copy (the context's upload buffer for host payloads).
+// `async`: return once the copies are enqueued on the context stream.
 static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool src_dev, size_t bytes, uint32_t dm,
-                                     uint32_t dn, uint32_t bits, uint32_t layout) {
+                                     uint32_t dn, uint32_t bits, uint32_t layout, bool async = false) {
   if (!ctx) return nullptr;
   if (!src) {
     fail(ctx, PRISM_HIP_ERR_NULL, "payload is NULL");
@@ -791,36 +871,50 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
   w->layout = layout;
   w->bytes = bytes;
   w->gi64 = gi64_layout(ctx, dm, dn, bits);
-  hipError_t e = hipMalloc(&w->d, w->gi64 ? prism::gi64_bytes(dm, dn) : bytes);
-  void* tmp = nullptr;
-  if (!w->gi64) {
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(w->d, src, bytes, src_dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
-  } else {
-    // regroup the split-block payload on the device (a host payload is
-    // staged in a temporary device buffer first)
-    const void* s = src;
-    if (e == hipSuccess && !src_dev) {
-      e = hipMalloc(&tmp, bytes);
-      if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, bytes, hipMemcpyHostToDevice, ctx->stream);
-      s = tmp;
+  auto bail = [&](int rc) -> prism_hip_weight* {
+    (void)rc;
+    if (w->d) {
+      (void)hipStreamSynchronize(ctx->stream);
+      (void)hipFree(w->d);
     }
-    if (e == hipSuccess) {
+    delete w;
+    return nullptr;
+  };
+  hipError_t e = hipMalloc(&w->d, w->gi64 ? prism::gi64_bytes(dm, dn) : bytes);
+  if (e != hipSuccess) {
+    w->d = nullptr;
+    fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload (%zu bytes): hipMalloc: %s", bytes, hipGetErrorString(e));
+    return bail(PRISM_HIP_ERR_DEVICE);
+  }
+  int rc = PRISM_HIP_OK;
+  const void* s = src;
+  if (!w->gi64) {
+    if (src_dev) {
+      e = hipMemcpyAsync(w->d, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
+      if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload: %s", hipGetErrorString(e));
+    } else {
+      rc = stage_h2d(ctx, w->d, src, bytes);
+    }
+  } else {
+    if (!src_dev) {
+      rc = ensure_upload_stage(ctx, bytes);
+      if (rc == PRISM_HIP_OK) rc = stage_h2d(ctx, ctx->d_upload, src, bytes);
+      s = ctx->d_upload;
+    }
+    if (rc == PRISM_HIP_OK) {
       const size_t pieces = prism::gi64_bytes(dm, dn) / 16;
       const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
       hipLaunchKernelGGL(prism::k_gi64_pack, dim3(grid), dim3(256), 0, ctx->stream,
                          reinterpret_cast<const uint8_t*>(s), w->d, dm, dn);
       e = hipGetLastError();
+      if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "GI64 pack: %s", hipGetErrorString(e));
     }
   }
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  if (tmp) (void)hipFree(tmp);
-  if (e != hipSuccess) {
-    fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload (%zu bytes): %s", bytes, hipGetErrorString(e));
-    if (w->d) (void)hipFree(w->d);
-    delete w;
-    return nullptr;
+  if (rc == PRISM_HIP_OK && (!async || src_dev)) {
+    e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload (%zu bytes): %s", bytes, hipGetErrorString(e));
   }
+  if (rc != PRISM_HIP_OK) return bail(rc);
   ctx->weights.insert(w);
   ctx->err.clear();
   return w;
@@ -831,9 +925,22 @@ prism_hip_weight* prism_hip_weight_upload(prism_hip_ctx* ctx, const uint8_t* pay
   return upload_impl(ctx, payload, false, bytes, dim_m, dim_n, bits, layout);
 }
 
+prism_hip_weight* prism_hip_weight_upload_async(prism_hip_ctx* ctx, const uint8_t* payload, size_t bytes,
+                                                uint32_t dim_m, uint32_t dim_n, uint32_t bits, uint32_t layout) {
+  return upload_impl(ctx, payload, false, bytes, dim_m, dim_n, bits, layout, true);
+}
+
 prism_hip_weight* prism_hip_weight_upload_dev(prism_hip_ctx* ctx, const void* d_payload, size_t bytes, uint32_t dim_m,
                                               uint32_t dim_n, uint32_t bits, uint32_t layout) {
   return upload_impl(ctx, d_payload, true, bytes, dim_m, dim_n, bits, layout);
+}
+
+int prism_hip_ctx_synchronize(prism_hip_ctx* ctx) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  DeviceGuard g(ctx->device);
+  HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+  ctx->err.clear();
+  return PRISM_HIP_OK;
 }
 
 void prism_hip_weight_free(prism_hip_weight* w) {
