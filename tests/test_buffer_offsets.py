@@ -1,0 +1,212 @@
+"""Buffer-load offsets of the HIP kernels, modelled on the CPU.
+
+gfx9-family raw buffer loads range-check only the per-lane VGPR offset
+(plus the instruction's immediate offset) against the descriptor's
+num_records; the scalar offset is added after the check.  A load whose VGPR
+offset is in range therefore touches memory at base + voffset + soffset,
+and that must lie inside the allocation even though the hardware does not
+check the soffset part.  A load whose VGPR offset is out of range returns
+zeros and touches nothing.
+
+For every buffer load of the kernels that take one, and for the launch
+shapes the library's dispatch gives them, these tests enumerate each lane's
+(voffset, soffset) pairs from the kernel's own index arithmetic (cited by
+file and line) and assert:
+  * every performed load (voffset < num_records) ends inside the
+    allocation: voffset + soffset + width <= allocation bytes;
+  * every performed load of row-structured data stays inside its own row
+    (it reads the row the lane owns, not the next one);
+  * rows past the end of the matrix (or of X) are never performed loads.
+Kernel constants are read from the headers, so a change there is seen here.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+
+CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "prism-engine_amd", "csrc")
+
+
+def _const(header: str, name: str) -> int:
+    with open(os.path.join(CSRC, header)) as f:
+        text = f.read()
+    m = re.search(r"constexpr int " + name + r"\s*=\s*([^;]+);", text)
+    assert m, f"{name} not found in {header}"
+    expr = m.group(1)
+    # resolve references to other constants of the same header
+    for ref in re.findall(r"[A-Za-z_]\w*", expr):
+        if ref != name:
+            expr = expr.replace(ref, str(_const(header, ref)))
+    return int(eval(expr, {"__builtins__": {}}))
+
+
+GW4_BN = _const("gemm_kernels.hpp", "GW4_BN")
+GW4_BK = _const("gemm_kernels.hpp", "GW4_BK")
+GI_ROWS = _const("gemv_kernels.hpp", "kGiRows")
+GI_LUT = _const("gemv_kernels.hpp", "kGiLutBytes")
+GM_TILES = _const("gemv_mfma.hpp", "kGmTiles")
+GM_ROWS = _const("gemv_mfma.hpp", "kGmRows")
+GM_WAVES = _const("gemv_mfma.hpp", "kGmWaves")
+GM_GROUP = _const("gemv_mfma.hpp", "kGmGroup")
+
+
+def gi64_group_bytes(K):
+    return GI_LUT + GI_ROWS * (K // 2)
+
+
+def gi64_bytes(N, K):
+    return -(-N // GI_ROWS) * gi64_group_bytes(K)
+
+
+def _check(voff, soff, width, num_records, alloc, what):
+    voff = np.asarray(voff, dtype=np.int64)
+    soff = np.broadcast_to(np.asarray(soff, dtype=np.int64), voff.shape)
+    performed = voff < num_records
+    end = voff + soff + width
+    bad = performed & (end > alloc)
+    assert not bad.any(), f"{what}: {int(bad.sum())} loads end past the {alloc}-byte allocation " \
+                          f"(first voff {int(voff[bad][0])}, soff {int(soff[bad][0])})"
+    return performed
+
+
+# ---- k_gemm_w4 (gemm_kernels.hpp:470-503): X and index DMA of every block
+def _tiles(mt, nt):
+    """Every tile of a small grid; for a large one the tiles of the first and
+    last M and N blocks (where the ends of X and W are) and a few others."""
+    if mt * nt <= 64:
+        return range(mt * nt)
+    keep = {m * nt + n for m in (0, mt - 1) for n in range(nt)} | {m * nt + n for m in range(mt) for n in (0, nt - 1)}
+    keep |= set(np.random.default_rng(0).integers(0, mt * nt, 16).tolist())
+    return sorted(keep)
+
+
+def _gemm_w4(M, N, K, MI, GI):
+    BM, BN, BK = 32 * MI, GW4_BN, GW4_BK
+    XR = 8 * MI
+    lane = np.arange(64)[:, None]
+    lr8, lc = lane >> 3, (lane & 7) ^ (lane >> 3)
+    row_bytes = K // 2
+    its = np.arange(K // BK)[None, :]  # K steps (the scalar offset)
+    mt, nt = -(-M // BM), -(-N // BN)
+    x_alloc = M * K * 2
+    w_alloc = gi64_bytes(N, K) if GI else N * row_bytes
+    for t in _tiles(mt, nt):
+        n0, m0 = (t % nt) * BN, (t // nt) * BM
+        live = min(M - m0, BM)
+        x_base = m0 * K * 2  # the descriptor's base is X + m0 * K
+        for wave in range(4):
+            xv0 = (XR * wave + lr8) * K * 2 + 16 * lc
+            for i in range(MI):
+                xv = ((xv0 ^ 16) if (i & 1) else xv0) + i * 16 * K
+                row = XR * wave + lr8 + 8 * i  # row of the block this lane's DMA reads
+                xvb, soff = np.broadcast_arrays(xv, its * 128)
+                perf = _check(xvb, soff, 16, live * K * 2, x_alloc - x_base, f"gemm_w4 X M={M} t={t}")
+                rowb = np.broadcast_to(row, xvb.shape)
+                assert not (perf & (rowb >= live)).any(), "a row past M is read"
+                ok = (xvb + soff + 16 <= (rowb + 1) * K * 2) & (xvb + soff >= rowb * K * 2)
+                assert ok[perf].all(), "an X load leaves its row"
+            if GI:
+                g = (n0 + 64 * wave) // GI_ROWS
+                wv0 = g * gi64_group_bytes(K) + GI_LUT + lane * 16
+                wvs = [wv0, wv0 + 1024]
+                grp_end = (g + 1) * gi64_group_bytes(K)
+            else:
+                rows = n0 + 64 * wave + (lane >> 1)
+                wv0 = rows * row_bytes + 16 * (lane & 1)
+                wvs = [wv0, wv0 + 32 * row_bytes]
+            for i, wv in enumerate(wvs):
+                wvb, soff = np.broadcast_arrays(wv, its * (2048 if GI else 32))
+                perf = _check(wvb, soff, 16, w_alloc, w_alloc, f"gemm_w4 W N={N} t={t} GI={GI}")
+                if GI:
+                    assert (wvb + soff + 16 <= grp_end)[perf].all(), "a GI64 load leaves its group"
+                else:
+                    r = np.broadcast_to(rows + 32 * i, wvb.shape)
+                    assert not (perf & (r >= N)).any(), "a weight row past N is read"
+                    assert (wvb + soff + 16 <= (r + 1) * row_bytes)[perf].all(), "an index load leaves its row"
+
+
+@pytest.mark.parametrize("M,N,K,MI,GI", [
+    (2048, 14336, 4096, 8, False), (2048, 14336, 4096, 8, True),
+    (300, 9000, 2048, 4, True), (200, 2000, 2048, 8, False), (96, 2000, 2048, 4, False),
+    (33, 4864, 896, 2, False), (600, 4096, 1024, 8, False), (65, 4099, 1024, 2, False),
+])
+def test_gemm_w4_offsets(M, N, K, MI, GI):
+    _gemm_w4(M, N, K, MI, GI)
+
+
+# ---- k_gemv_mfma (gemv_mfma.hpp:75-110): x rows and index groups
+@pytest.mark.parametrize("N,K,nb,bits,GI", [
+    (14336, 4096, 8, 4, True), (14336, 4096, 16, 4, False), (14336, 4096, 5, 8, False),
+    (4099, 1024, 3, 4, False), (9000, 2048, 16, 4, True), (1000, 384, 4, 8, False),
+])
+def test_gemv_mfma_offsets(N, K, nb, bits, GI):
+    lane = np.arange(64)
+    n, kq = lane & 15, lane >> 4
+    IB = 32 * bits // 8
+    ng = K // GM_GROUP
+    x_alloc = nb * K * 2
+    wbytes = gi64_bytes(N, K) if GI else N * (K * bits // 8)
+    row_b = K * bits // 8
+    for blk in range(-(-N // GM_ROWS)):
+        n0 = blk * GM_ROWS
+        for wave in range(GM_WAVES):
+            mine = (ng - wave + GM_WAVES - 1) // GM_WAVES if ng > wave else 0
+            for g in range(mine):
+                k0 = (wave + GM_WAVES * g) * GM_GROUP
+                xv = n * K * 2 + kq * 64
+                for j in range(4):
+                    perf = _check(xv + 16 * j, k0 * 2, 16, x_alloc, x_alloc, "gemv_mfma x")
+                    assert ((xv + 16 * j + k0 * 2 + 16) <= (n + 1) * K * 2)[perf].all(), "x load leaves its row"
+                    assert not (perf & (n >= nb)).any()
+                for t in range(GM_TILES):
+                    r = np.minimum(n0 + 16 * t + n, N - 1)
+                    if GI:
+                        iv = (r // GI_ROWS) * gi64_group_bytes(K) + GI_LUT + (kq * GI_ROWS + r % GI_ROWS) * 16
+                        soff = k0 * 32
+                        end = (r // GI_ROWS + 1) * gi64_group_bytes(K)
+                    else:
+                        iv = r * row_b + kq * IB
+                        soff = k0 * bits // 8
+                        end = (r + 1) * row_b
+                    for j in range(IB // 16):
+                        perf = _check(iv + 16 * j, soff, 16, wbytes, wbytes, "gemv_mfma index")
+                        assert ((iv + 16 * j + soff + 16) <= end)[perf].all(), "index load leaves its row/group"
+
+
+# ---- k_gemv_tile (gemv_tile.hpp:229-262) and k_gemv_lpr (gemv_lpr.hpp:120-135):
+# every offset is in the VGPR part; a performed load must end inside the
+# allocation (the range check is per load, so alignment matters)
+@pytest.mark.parametrize("N,K,bits", [(14336, 4096, 4), (4864, 896, 4), (151936, 896, 4), (3, 1024, 4),
+                                      (14336, 4096, 8), (31, 48, 8), (100, 2080, 4)])
+def test_gemv_tile_offsets_are_aligned(N, K, bits):
+    # x: 16-byte loads at (tid + T t) * 16 against K * 2 bytes
+    units = np.arange(0, (K // 8) + 64)
+    _check(units * 16, 0, 16, K * 2, K * 2, "gemv_tile x")
+    # index: IW dwords per unit, rows clamped to N - 1
+    IW = 1 if bits == 4 else 2
+    row_dw = K * bits // 32
+    for rc in (0, N - 1):
+        vo = rc * row_dw * 4 + units * 4 * IW
+        perf = _check(vo, 0, 4 * IW, N * row_dw * 4, N * row_dw * 4, "gemv_tile index")
+        live = units < K // 8
+        assert ((vo + 4 * IW) <= (rc + 1) * row_dw * 4)[perf & live].all()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048), (16384, 2048), (8192, 2112)])
+def test_gemv_lpr_offsets(N, K):
+    """Chunk c of wave w's range, or an offset past the range (0x80000000)."""
+    NC = K // 32
+    lane = np.arange(64)
+    nbytes = gi64_bytes(N, K)
+    for S in (8, 16):
+        for w in range(S):
+            c0, nch = (w * NC) // S, ((w + 1) * NC) // S - (w * NC) // S
+            for g in (0, -(-N // GI_ROWS) - 1):
+                vbase = g * gi64_group_bytes(K) + GI_LUT + (c0 * GI_ROWS + lane) * 16
+                for i in range(nch + 8):  # the ring issues up to P loads past the range
+                    vo = vbase + i * 1024 if i < nch else np.full(64, 0x80000000)
+                    perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr chunk")
+                    assert perf.all() == (i < nch)
+                    if i < nch:
+                        assert ((vo + 16) <= (g + 1) * gi64_group_bytes(K)).all()
