@@ -23,6 +23,7 @@
 #include <stdint.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "gemv_lpr.hpp"
 #include "lut_perm.hpp"
@@ -366,7 +367,7 @@ constexpr int kGwdWord3 = 0x00020000;
 //   k = 64 it + 32h + 8q + 0..7, and the A fragment of the same lane holds
 //   the same k (logical chunk 4h + q of the X tile row).
 // * Both global streams -- the X tile and the index chunks -- are fetched
-//   by the LDS DMA (buffer_load ... lds) into a GWD_STAGES-deep ring of LDS
+//   by the LDS DMA (buffer_load ... lds) into a ring of gwd_stages<MI>() LDS
 //   stages, so no VGPR-destination global load is left in the K loop:
 //   - X part of a stage: 256 rows x 64 halves = 2048 16-byte slots,
 //     unpadded; slot (r, p) holds logical chunk p ^ f(r) of row r, f(r) =
@@ -383,13 +384,14 @@ constexpr int kGwdWord3 = 0x00020000;
 //   - index part: 256 weight rows x 32 bytes (this K step's 64 nibbles),
 //     2 slots per row; wave w fills its own 64 rows with 2 instructions,
 //     the row again in the VGPR offset and the K step in the scalar one.
-// * Schedule of K step it (stage it % 3): MFMA steps 0..2 each read the next
-//   step's A fragments and decode its B operands (double buffers) under
-//   their own 16 MFMAs.  Before MFMA step 3 the wave waits for its reads of
-//   the stage (lgkmcnt) and for its own DMA of step it+1 (loads return in
-//   issue order, so vmcnt <= the 10 instructions of step it+2); the barrier
-//   then publishes step it+1's stage and frees stage it % 3, which the
-//   wave refills with step it+3.  Step it+1's index chunks and first A
+// * Schedule of K step it (stage it % S, S = gwd_stages<MI>()): MFMA steps
+//   0..2 each read the next step's A fragments and decode its B operands
+//   (double buffers) under their own MFMAs.  Before MFMA step 3 the wave
+//   waits for its reads of the stage (lgkmcnt) and for its own DMA of step
+//   it+1 (loads return in issue order, so vmcnt <= the instructions of the
+//   up to S-2 steps issued after it); the barrier then publishes step
+//   it+1's stage and frees stage it % S, which the wave refills with step
+//   it+S.  Step it+1's index chunks and first A
 //   fragments are read under step 3's MFMAs and its first B operands are
 //   decoded after them, while the matrix core drains the queued MFMAs.
 // * Blocks are mapped XCD-aware: hardware dispatches block b to XCD b % 8;
@@ -399,8 +401,15 @@ constexpr int kGwdWord3 = 0x00020000;
 // 256 * K * 2 bytes of X per block below 2 GiB (the buffer descriptors'
 // 32-bit ranges; rows past M or N read as 0 through the range check of the
 // VGPR offset).
-constexpr int GWD_STAGES = 3;
 constexpr int GWD_WSLOTS = GW4_BN * 2;  // 16-byte index slots per stage
+// Ring depth (stages of the DMA ring).  Deeper rings for the shorter blocks
+// (6 stages of 24 KB for 128-row blocks, 8 of 16 KB for 64-row blocks)
+// measured no faster on short prefills (14336 x 4096, M = 64: 39.4 against
+// 37.2-38.0 us; M = 128..512 within 2 %), so every block height keeps 3.
+template <int MI>
+constexpr int gwd_stages() {
+  return 3;
+}
 
 __device__ __forceinline__ void gwd_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
@@ -423,6 +432,29 @@ __device__ __forceinline__ void gwd_wait_vm() {
   __builtin_amdgcn_s_waitcnt((N_ & 0xF) | ((N_ >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// vmcnt <= n * OPS for a wave-uniform n <= MAXN (the immediate is chosen by
+// a branch per value).
+template <int OPS, int MAXN>
+__device__ __forceinline__ void gwd_wait_steps(uint32_t n) {
+  if constexpr (MAXN > 0) {
+    if (n >= (uint32_t)MAXN) {
+      gwd_wait_vm<MAXN * OPS>();
+      return;
+    }
+    gwd_wait_steps<OPS, MAXN - 1>(n);
+  } else {
+    gwd_wait_vm<0>();
+  }
+}
+
+// f(integral_constant<int, I>, it + I) for each I with it + I < nk, as a
+// flat sequence of tests (nesting them kept more values live: the 256-row
+// kernel spilled).
+template <class F, int... I>
+__device__ __forceinline__ void gwd_steps(uint32_t it, uint32_t nk, F& f, std::integer_sequence<int, I...>) {
+  ((it + I < nk ? (f(std::integral_constant<int, I>{}, it + I), 0) : 0), ...);
+}
+
 // MI = 32-row M subtiles per block (BM = 32 MI): 8 for long prefills; 2 and
 // 4 give short ones (65..1024 rows) more blocks.
 // GI: the weights are in the GI64 layout (gemv_lpr.hpp; lut and idx both
@@ -437,7 +469,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
                                                  const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
                                                  uint32_t N, uint32_t K, float* __restrict__ P, uint32_t kps) {
   static_assert(MI == 2 || MI == 4 || MI == 8, "32-row M subtiles per block");
-  constexpr int BM = 32 * MI, BN = GW4_BN, BK = GW4_BK, S = GWD_STAGES;
+  constexpr int BM = 32 * MI, BN = GW4_BN, BK = GW4_BK, S = gwd_stages<MI>();
   constexpr int XS = BM * BK / 8;     // 16-byte X slots per stage
   constexpr int SL = XS + GWD_WSLOTS;
   constexpr int OPS = MI + 2;         // DMA instructions per wave per K step (MI X + 2 index)
@@ -533,23 +565,18 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     bop[buf][1] = decode_nib8_nat(wdword(wch[1], q), pl[1]);
   };
 
-  // Prologue: steps 0..2 in flight, step 0 landed everywhere.
-  issue(0, 0);
-  if (nk > 1) issue(1, 1);
-  if (nk > 2) issue(2, 2);
-  if (nk > 2)
-    gwd_wait_vm<2 * OPS>();
-  else if (nk > 1)
-    gwd_wait_vm<OPS>();
-  else
-    gwd_wait_vm<0>();
+  // Prologue: steps 0..S-1 in flight, step 0 landed everywhere.
+#pragma unroll
+  for (int u = 0; u < S; u++)
+    if ((uint32_t)u < nk) issue(u, u);
+  gwd_wait_steps<OPS, S - 1>((nk < (uint32_t)S ? nk : (uint32_t)S) - 1);
   gwd_barrier();
   read_first(sx);
   decode_b(0, 0);
 
   auto kstep = [&](auto sc_tag, uint32_t it) {
     constexpr int SC = decltype(sc_tag)::value;
-    constexpr int SNX = (SC + 1) % 3;
+    constexpr int SNX = (SC + 1) % S;
     const uint4* st = sx + SC * SL;
 #pragma unroll
     for (int q = 0; q < 3; q++) {
@@ -577,12 +604,11 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     // past the asm).
     asm volatile("" : "+v"(bop[1][0]), "+v"(bop[1][1]));
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of stage SC are done
-    if (it + 2 < nk)
-      gwd_wait_vm<OPS>();
-    else
-      gwd_wait_vm<0>();
+    // step it + 1 must have landed; the steps after it may stay in flight
+    const uint32_t ahead = it + 2 < nk ? (nk - it - 2 < (uint32_t)(S - 2) ? nk - it - 2 : (uint32_t)(S - 2)) : 0u;
+    gwd_wait_steps<OPS, S - 2>(ahead);
     gwd_barrier();
-    if (it + 3 < nk) issue(it + 3, SC);
+    if (it + S < nk) issue(it + S, SC);
     const bool more = it + 1 < nk;
     const uint4* sn = sx + SNX * SL;
     if (more) {
@@ -605,11 +631,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
     __builtin_amdgcn_sched_group_barrier(0x002, 64, 0);  // VALU: next step's decode
   };
 
-  for (uint32_t it = 0; it < nk; it += 3) {
-    kstep(std::integral_constant<int, 0>{}, it);
-    if (it + 1 < nk) kstep(std::integral_constant<int, 1>{}, it + 1);
-    if (it + 2 < nk) kstep(std::integral_constant<int, 2>{}, it + 2);
-  }
+  for (uint32_t it = 0; it < nk; it += S) gwd_steps(it, nk, kstep, std::make_integer_sequence<int, S>{});
 
   // ---- epilogue: D lane layout: col j = lane%32, row 8*(e/4) + 4*(lane/32) + e%4
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
