@@ -83,12 +83,15 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def gi64_layout(bits: int, N: int, K: int, num_cu: int) -> bool:
-    """The library's device-layout rule (prism_hip.hip gi64_layout): 4-bit
-    matrices with K % 64 == 0, K >= 2048 and num_cu/2 .. num_cu groups of 64
-    rows are regrouped to GI64 and run on the lane-per-row GEMV."""
-    groups = -(-N // 64)
-    return bits == 4 and K % 64 == 0 and K >= 2048 and 2 * groups >= num_cu and groups <= num_cu
+def gi_rows(bits: int, N: int, K: int, num_cu: int) -> int:
+    """The library's device-layout rule (prism_hip.hip gi_rows): 4-bit
+    matrices with K % 64 == 0 and K >= 2048 whose rows fill every CU in one
+    round of 32..64-row groups are regrouped to the GI layout (G rows per
+    group) and run on the lane-per-row GEMV.  Returns G, or 0."""
+    if bits != 4 or K % 64 or K < 2048:
+        return 0
+    G = (-(-N // num_cu) + 7) // 8 * 8
+    return G if 32 <= G <= 64 else 0
 
 
 def weight_bytes(bits: int, N: int, K: int) -> int:
@@ -368,7 +371,7 @@ def run_palettize(args, pe, seed) -> int:
 
 def run_load(args, pe, seed) -> int:
     """load_cimage timed end to end: mmap of the file, every palettized
-    tensor through the context's pinned staging ring (GI64 regrouping on
+    tensor through the context's pinned staging ring (GI regrouping on
     the device where it applies), one wait.  The file is a Qwen2.5-0.5B-
     sized 4-bit .cimage with random payload bytes, written to the host's
     temporary directory first (so it is read from the page cache)."""
@@ -632,21 +635,22 @@ def main() -> int:
             (5 <= batch <= 16 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
     # and its GEMM dispatch: prefills of up to 256 rows split K over one
     # 128- or 256-row block (at most 4 splits, at least 8 K steps each)
-    gi = gi64_layout(bits, N, K, torch.cuda.get_device_properties(0).multi_processor_count)
-    gemm4 = f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" + (" (GI64)" if gi else "")
+    gi = gi_rows(bits, N, K, torch.cuda.get_device_properties(0).multi_processor_count)
+    gtag = f" (GI{gi})" if gi else ""
+    gemm4 = f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" + gtag
     if bits == 4 and batch <= 256:
         smi = 4 if batch <= 128 else 8
         blocks = -(-batch // (32 * smi)) * -(-N // 256)
         sk = min(4, 256 // blocks, (K // 64) // 8)
         if sk >= 2:
-            gemm4 = f"k_gemm_w4<{smi}>{' (GI64)' if gi else ''} in {sk} K splits + k_gemm_split_sum"
+            gemm4 = f"k_gemm_w4<{smi}>{gtag} in {sk} K splits + k_gemm_split_sum"
     if gi:
-        gemv_name = ("k_gemv_lpr<8,1,%d> (GI64)" % batch if batch <= 2 else
-                     "k_gemv_mfma<4,GI64>" if K % 128 == 0 else "k_gemv_lpr<8,1,2> passes (GI64)")
+        gemv_name = (f"k_gemv_lpr<8,1,{batch}>{gtag}" if batch <= 2 else
+                     f"k_gemv_mfma<4,GI>{gtag}" if K % 128 == 0 else f"k_gemv_lpr<8,1,2> passes{gtag}")
     else:
         gemv_name = f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile"
     kernel_name = {"floor": "k_stream_read", "gemv": gemv_name,
-                   "gateup": "k_gemv_lpr<16,2,1,SwiGLU> (GI64)" if gi else "k_gemv_tile (DUAL gate_up + SwiGLU)",
+                   "gateup": f"k_gemv_lpr<16,2,1,SwiGLU>{gtag}" if gi else "k_gemv_tile (DUAL gate_up + SwiGLU)",
                    "gemm": ("GEMV passes" if batch <= (48 if bits == 8 else 32) else
                             gemm4 if bits == 4 else
                             "k_gemm8" if batch > 256 and K % 64 == 0 else

@@ -208,7 +208,8 @@ constexpr int GM8_BK = 64;
 template <bool SPLIT>
 __global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
-                                               uint32_t N, uint32_t K, float* __restrict__ part, uint32_t kps) {
+                                               uint32_t N, uint32_t K, float* __restrict__ part, uint32_t kps,
+                                               uint32_t /* G: the GI layout's group rows, 4-bit only */) {
   constexpr int BM = GM8_BM, BN = GM8_BN, BK = GM8_BK, P = BK + 8;
   constexpr int XU = BM * BK / 8 / 256;  // 16-byte X chunks per thread per step (8)
   constexpr int WU = BN * BK / 16 / 256; // 16-byte index chunks per thread per step (2)
@@ -457,17 +458,19 @@ __device__ __forceinline__ void gwd_steps(uint32_t it, uint32_t nk, F& f, std::i
 
 // MI = 32-row M subtiles per block (BM = 32 MI): 8 for long prefills; 2 and
 // 4 give short ones (65..1024 rows) more blocks.
-// GI: the weights are in the GI64 layout (gemv_lpr.hpp; lut and idx both
-// point at it).  Wave w's 64 rows are one GI64 group, so a K step's index
-// bytes are two contiguous 1 KB chunks (one DMA instruction each, lane l ->
-// row l) and slot (c, r) of the index part holds chunk c of row r.
+// GI: the weights are in the GI layout with G rows per group (gemv_lpr.hpp;
+// lut and idx both point at it).  A K step's index bytes of a row are two
+// 16-byte chunks; DMA instruction i of wave w carries chunk i of its 64 rows
+// (lane l -> row 64 w + l; G consecutive rows' chunks are contiguous), and
+// slot (c, r) of the index part holds chunk c of row r.
 // SPLIT: block (x, y) covers K steps [y kps, min(K / 64, (y + 1) kps)) and
 // writes its fp32 partial tile to P[y][M][N] (k_gemm_split_sum adds the
 // partials); otherwise the whole K range, fp16 to Y.
 template <int MI, bool SPLIT, bool GI = false>
 __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                  const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
-                                                 uint32_t N, uint32_t K, float* __restrict__ P, uint32_t kps) {
+                                                 uint32_t N, uint32_t K, float* __restrict__ P, uint32_t kps,
+                                                 uint32_t G) {
   static_assert(MI == 2 || MI == 4 || MI == 8, "32-row M subtiles per block");
   constexpr int BM = 32 * MI, BN = GW4_BN, BK = GW4_BK, S = gwd_stages<MI>();
   constexpr int XS = BM * BK / 8;     // 16-byte X slots per stage
@@ -503,7 +506,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   for (int s = 0; s < 2; s++) {
     uint32_t n = n0 + 64 * wave + 32 * s + j;
     n = n < N ? n : N - 1;
-    const uint4* lr = reinterpret_cast<const uint4*>(lut + (GI ? gi64_lut_offset(n, K) : (size_t)n * 32));
+    const uint4* lr = reinterpret_cast<const uint4*>(lut + (GI ? gi_lut_offset(G, n, K) : (size_t)n * 32));
     pl[s] = make_planes(lr[0], lr[1]);
   }
   // ---- DMA sources; reads past the descriptors' ranges return 0
@@ -511,7 +514,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(X + (size_t)m0 * K), (short)0, (int)(live * K * 2u), kGwdWord3);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)idx, (short)0, (int)(GI ? (uint32_t)gi64_bytes(N, K) : N * row_bytes), kGwdWord3);
+      (void*)idx, (short)0, (int)(GI ? (uint32_t)gi_bytes(G, N, K) : N * row_bytes), kGwdWord3);
   const uint32_t lr8 = (uint32_t)lane >> 3, lc = ((uint32_t)lane & 7u) ^ lr8;
   // Per-lane VGPR offsets of each DMA instruction (row and chunk); the
   // scalar offset carries only the K step.
@@ -519,19 +522,20 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   uint32_t xv[MI];
 #pragma unroll
   for (int i = 0; i < MI; i++) xv[i] = ((i & 1) ? (xv0 ^ 16u) : xv0) + (uint32_t)i * 16u * K;  // odd: chunk lc ^ 1
-  // GI64: instruction i reads chunk 2 (it + kb) + i of the wave's group (the
-  // group base is past the range for groups past N: zeros)
-  const uint32_t wv0 = GI ? (uint32_t)((size_t)((n0 + 64u * wave) / kGiRows) * gi64_group_bytes(K)) + kGiLutBytes +
-                                (uint32_t)lane * 16u
+  // GI: instruction i reads chunk 2 (it + kb) + i of row 64 w + l (rows past
+  // N get an offset past the range: zeros); a K step moves 2 chunks
+  const uint32_t grow = n0 + 64u * wave + (uint32_t)lane;
+  const uint32_t wv0 = GI ? (grow < N ? (uint32_t)gi_chunk_offset(G, grow, 0, K) : 0x80000000u)
                           : (n0 + 64u * wave + ((uint32_t)lane >> 1)) * row_bytes + 16u * ((uint32_t)lane & 1u);
-  const uint32_t wv[2] = {wv0, GI ? wv0 + 1024u : wv0 + 32u * row_bytes};
+  const uint32_t wv[2] = {wv0, GI ? wv0 + G * (uint32_t)kGiChunk : wv0 + 32u * row_bytes};
 
   auto issue = [&](uint32_t it, int stage) {
     uint4* st = sx + stage * SL;
 #pragma unroll
     for (int i = 0; i < MI; i++) gwd_dma16(rx, st + 64 * (MI * wave + i), xv[i], (it + kb) * 128u);
 #pragma unroll
-    for (int i = 0; i < 2; i++) gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv[i], (it + kb) * (GI ? 2048u : 32u));
+    for (int i = 0; i < 2; i++)
+      gwd_dma16(rw, st + XS + 64 * (2 * wave + i), wv[i], (it + kb) * (GI ? 2u * G * (uint32_t)kGiChunk : 32u));
   };
   auto wdword = [](const uint4& v, int q) { return q == 0 ? v.x : q == 1 ? v.y : q == 2 ? v.z : v.w; };
 

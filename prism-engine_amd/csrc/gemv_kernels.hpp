@@ -58,41 +58,42 @@ struct GemvArgs {
   uint32_t nb;          // live batch rows (<= NB)
   float eps;            // RMS-norm epsilon (k_gemv_tile with kEpiNorm)
   const float* xpart;   // attention split partials (k_gemv_tile with kEpiAttnIn)
+  uint32_t gi;          // GI layout: rows per group (kernels instantiated for GI)
 };
 
 // Generic kernel for shapes the tiled kernel does not take (K % 8 != 0,
 // unaligned x): one wave per row, element-strided.  Follows lut_gemv_cpu's
 // ragged-K rule for 4-bit weights: row stride K/2 bytes, only the first
 // (K/8)*8 elements contribute.
-// GI64: the group-interleaved 4-bit device layout (k_gemv_lpr, gemv_lpr.hpp,
-// describes it): ceil(N/64) groups of [64 x 32 B LUTs][K/32 chunks][64
-// rows][16 B], rows past N zero.
-constexpr int kGiRows = 64;                // rows per group
-constexpr int kGiChunk = 16;               // index bytes per chunk (32 elements)
-constexpr int kGiLutBytes = kGiRows * 32;  // LUT block at the start of a group
+// GI: the group-interleaved 4-bit device layout (k_gemv_lpr, gemv_lpr.hpp,
+// describes it): ceil(N/G) groups of [G x 32 B LUTs][K/32 chunks][G
+// rows][16 B], rows past N zero, G <= kGiMaxRows rows per group (one per
+// lane of a wave).
+constexpr int kGiMaxRows = 64;  // rows per group at most
+constexpr int kGiChunk = 16;    // index bytes per chunk (32 elements)
 
-__host__ __device__ __forceinline__ size_t gi64_group_bytes(uint32_t K) {
-  return (size_t)kGiLutBytes + (size_t)kGiRows * (K / 2);
+__host__ __device__ __forceinline__ size_t gi_group_bytes(uint32_t G, uint32_t K) {
+  return (size_t)G * 32 + (size_t)G * (K / 2);
 }
-__host__ __device__ __forceinline__ size_t gi64_bytes(uint32_t N, uint32_t K) {
-  return (size_t)((N + kGiRows - 1) / kGiRows) * gi64_group_bytes(K);
+__host__ __device__ __forceinline__ size_t gi_bytes(uint32_t G, uint32_t N, uint32_t K) {
+  return (size_t)((N + G - 1) / G) * gi_group_bytes(G, K);
 }
 // Byte offset of row r's LUT, of its chunk c, and of the byte holding its
 // element k.
-__host__ __device__ __forceinline__ size_t gi64_lut_offset(uint32_t r, uint32_t K) {
-  return (size_t)(r / kGiRows) * gi64_group_bytes(K) + (size_t)(r % kGiRows) * 32;
+__host__ __device__ __forceinline__ size_t gi_lut_offset(uint32_t G, uint32_t r, uint32_t K) {
+  return (size_t)(r / G) * gi_group_bytes(G, K) + (size_t)(r % G) * 32;
 }
-__host__ __device__ __forceinline__ size_t gi64_chunk_offset(uint32_t r, uint32_t c, uint32_t K) {
-  return (size_t)(r / kGiRows) * gi64_group_bytes(K) + kGiLutBytes +
-         ((size_t)c * kGiRows + (r % kGiRows)) * kGiChunk;
+__host__ __device__ __forceinline__ size_t gi_chunk_offset(uint32_t G, uint32_t r, uint32_t c, uint32_t K) {
+  return (size_t)(r / G) * gi_group_bytes(G, K) + (size_t)G * 32 + ((size_t)c * G + (r % G)) * kGiChunk;
 }
-__host__ __device__ __forceinline__ size_t gi64_index_at(uint32_t r, uint32_t k, uint32_t K) {
-  return gi64_chunk_offset(r, k / 32, K) + (k % 32) / 2;
+__host__ __device__ __forceinline__ size_t gi_index_at(uint32_t G, uint32_t r, uint32_t k, uint32_t K) {
+  return gi_chunk_offset(G, r, k / 32, K) + (k % 32) / 2;
 }
 
 // MODE: kGenSingle, or gate + up rows (lut2/idx2) with the SwiGLU
 // epilogue (kGenSwiglu) or the two raw outputs y, y2 (kGenPair).
-// GI: 4-bit weights in the GI64 layout (a.lut and a.idx both point at it).
+// GI: 4-bit weights in the GI layout with a.gi rows per group (a.lut and
+// a.idx both point at it).
 constexpr int kGenSingle = 0, kGenSwiglu = 1, kGenPair = 2;
 template <int BITS, int MODE, bool GI = false>
 __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
@@ -107,13 +108,13 @@ __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
   for (uint32_t b = 0; b < nb; b++) {
     float acc[NM];
     for (int m = 0; m < NM; m++) {
-      const uint8_t* lut = (m == 0 ? a.lut : a.lut2) + (GI ? gi64_lut_offset(row, K) : (size_t)row * (2u << BITS));
+      const uint8_t* lut = (m == 0 ? a.lut : a.lut2) + (GI ? gi_lut_offset(a.gi, row, K) : (size_t)row * (2u << BITS));
       const uint8_t* idx = (m == 0 ? a.idx : a.idx2) + (GI ? 0 : (size_t)row * stride);
       float s = 0.0f;
       for (uint32_t k = lane; k < keff; k += 64) {
         uint32_t e;
         if (BITS == 4) {
-          const uint8_t byte = GI ? idx[gi64_index_at(row, k, K)] : idx[k >> 1];
+          const uint8_t byte = GI ? idx[gi_index_at(a.gi, row, k, K)] : idx[k >> 1];
           e = (k & 1) ? (byte >> 4) : (byte & 15u);
         } else {
           e = idx[k];
@@ -140,10 +141,12 @@ __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
 // (the per-row form of lut_embed, compute-core/src/lut/evaluator.rs:176-197).
 // For 4-bit weights elements at k >= (K/8)*8 are written as 0, matching
 // lut_embed's shorter output zero-padded.
-// GI: 4-bit weights in the GI64 layout (lut and idx both point at it).
+// GI: 4-bit weights in the GI layout with G rows per group (lut and idx
+// both point at it).
 template <int BITS, bool GI = false>
 __global__ __launch_bounds__(256) void k_decode_rows(const uint8_t* lut, const uint8_t* idx, uint32_t N,
-                                                     uint32_t K, uint32_t row0, uint32_t nrows, uint16_t* out) {
+                                                     uint32_t K, uint32_t row0, uint32_t nrows, uint16_t* out,
+                                                     uint32_t G) {
   const uint32_t stride = (BITS == 4) ? K / 2 : K;
   const uint32_t keff = (BITS == 4) ? (K / 8) * 8 : K;
   const size_t total = (size_t)nrows * K;
@@ -155,12 +158,12 @@ __global__ __launch_bounds__(256) void k_decode_rows(const uint8_t* lut, const u
     if (r < N && k < keff) {
       uint32_t e;
       if (BITS == 4) {
-        const uint8_t byte = GI ? idx[gi64_index_at(r, k, K)] : idx[(size_t)r * stride + (k >> 1)];
+        const uint8_t byte = GI ? idx[gi_index_at(G, r, k, K)] : idx[(size_t)r * stride + (k >> 1)];
         e = (k & 1) ? (byte >> 4) : (byte & 15u);
       } else {
         e = idx[(size_t)r * stride + k];
       }
-      const uint8_t* l = lut + (GI ? gi64_lut_offset(r, K) : (size_t)r * (2u << BITS)) + 2 * e;
+      const uint8_t* l = lut + (GI ? gi_lut_offset(G, r, K) : (size_t)r * (2u << BITS)) + 2 * e;
       v = (uint16_t)(l[0] | (l[1] << 8));
     }
     out[t] = v;

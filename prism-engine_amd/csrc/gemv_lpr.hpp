@@ -1,5 +1,5 @@
 // gemv_lpr.hpp -- lane-per-row palettized GEMV for gfx950 over the
-// group-interleaved 4-bit device layout (GI64), and the layout itself.
+// group-interleaved 4-bit device layout (GI), and the layout itself.
 //
 // y[b, r] = f16( sum_k f32(x[b, k]) * f32(LUT_r[idx(r, k)]) ): the
 // arithmetic of lut_gemv_cpu (compute-core/src/lut/evaluator.rs:21-44),
@@ -8,20 +8,22 @@
 // the CPU path (evaluator.rs:78-83,209-225, engine_impl.rs:1349-1374) or the
 // two raw outputs of fused_gate_up.metal (templates/fused_gate_up.metal:16-97).
 //
-// GI64 device layout (written at upload by k_gi64_pack, 4-bit, K % 64 == 0):
-//   ceil(N/64) row groups of gi64_group_bytes(K) bytes each:
-//     [64 x 32 B fp16 LUTs of the group's rows][K/32 chunks][64 rows][16 B]
+// GI device layout (written at upload by k_gi_pack, 4-bit, K % 64 == 0),
+// G <= 64 rows per group, chosen at upload so that the groups fill the GPU:
+//   ceil(N/G) row groups of gi_group_bytes(G, K) bytes each:
+//     [G x 32 B fp16 LUTs of the group's rows][K/32 chunks][G rows][16 B]
 //   chunk c of row r holds index bytes 16c .. 16c+15 of the split-block row
 //   (elements 32c .. 32c+31, element 2i = low nibble of byte i).  Rows past
 //   N in the last group are zero.  A wave's 16-byte-per-lane load reads
-//   chunk c of 64 consecutive rows: 1 KB contiguous.  A group's LUTs sit
-//   right before its chunks, so they come from the same DRAM pages as the
-//   first chunks (in a separate block the LUT requests returned late, behind
-//   the index stream).  Bytes are the split-block payload's, rearranged
-//   (plus the zero rows of the last group).
+//   chunk c of the group's G rows: 16 G bytes contiguous.  A group's LUTs
+//   sit right before its chunks, so they come from the same DRAM pages as
+//   the first chunks (in a separate block the LUT requests returned late,
+//   behind the index stream).  Bytes are the split-block payload's,
+//   rearranged (plus the zero rows of the last group).
 //
-// Work layout: one workgroup of S waves per group.  Lane l owns row
-// 64 g + l for the whole kernel; wave w owns a contiguous range of the
+// Work layout: one workgroup of S waves per group.  Lane l < G owns row
+// G g + l for the whole kernel (lanes past G load nothing and store
+// nothing); wave w owns a contiguous range of the
 // row's chunks (the S ranges partition K/32), so every lane of a wave
 // reads the same x elements at the same time and x lives in SGPRs
 // (scalar loads; v_dot2 takes it as its scalar operand).
@@ -56,7 +58,7 @@
 
 namespace prism {
 
-constexpr int kLprTableDw = 256 * kGiRows;  // dwords of one group's pair tables (64 KB)
+constexpr int kLprTableDw = 256 * 64;  // dwords of one workgroup's pair tables (64 KB, one per lane)
 
 // Epilogues of k_gemv_lpr.
 constexpr int kLprPlain = 0;   // y[b][row] = f16(acc)
@@ -64,7 +66,7 @@ constexpr int kLprSwiglu = 1;  // NM = 2: y[row] = swiglu(f16(gate), f16(up))
 constexpr int kLprPair = 2;    // NM = 2: y[row] = f16(gate), y2[row] = f16(up)
 
 struct LprArgs {
-  const uint8_t* w;    // GI64 weights
+  const uint8_t* w;    // GI weights
   const uint8_t* w2;   // NM = 2: up matrix, same shape
   const uint16_t* x;   // [nb][K] fp16
   uint16_t* y;         // [nb][N]
@@ -72,6 +74,7 @@ struct LprArgs {
   uint32_t N;
   uint32_t K;
   uint32_t nb;         // live batch vectors (<= NB)
+  uint32_t G;          // rows per group (<= 64)
 };
 
 template <int S, int NM, int NB, int EPI>
@@ -96,37 +99,44 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t g = blockIdx.x;
   const uint32_t N = a.N, K = a.K, NC = K / 32;
-  const uint32_t row = g * kGiRows + lane;
+  const uint32_t G = a.G;
+  const uint32_t row = g * G + lane;
+  const bool live = lane < G;
   const uint32_t c0 = (w * NC) / S, nch = ((w + 1) * NC) / S - c0;
-  const uint32_t gbase = g * (uint32_t)gi64_group_bytes(K);
+  const uint32_t gbytes = G * 32u + G * (K / 2);
+  const uint32_t gbase = g * gbytes;
+  __amdgpu_buffer_rsrc_t ri[NM];
+  const uint32_t nbytes = ((N + G - 1) / G) * gbytes;
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+    ri[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(m == 0 ? a.w : a.w2), (short)0, (int)nbytes, kBufferWord3);
 
   // ---- the LUT of the lane's row: 8 dwords, two 16-byte loads and nothing
   // else (the table build waits for them: a separate load of the low-nibble
   // entries a wave needs cost 0.4 us on the hero shape; they are picked out
   // of these registers below).  Lanes past N read the zero LUT slots of the
-  // last group's padding rows.
+  // last group's padding rows; lanes past G get an offset past the buffer's
+  // range and read zeros.
   uint32_t L[NM][8];
+  const uint32_t lo = live ? gbase + lane * 32u : 0x80000000u;
 #pragma unroll
   for (int m = 0; m < NM; m++) {
-    const uint8_t* lb = (m == 0 ? a.w : a.w2) + gbase + lane * 32u;
-    const uint4 l0 = reinterpret_cast<const uint4*>(lb)[0], l1 = reinterpret_cast<const uint4*>(lb)[1];
+    const u32x4v l0 = __builtin_amdgcn_raw_buffer_load_b128(ri[m], lo, 0u, 0);
+    const u32x4v l1 = __builtin_amdgcn_raw_buffer_load_b128(ri[m], lo + 16u, 0u, 0);
     L[m][0] = l0.x; L[m][1] = l0.y; L[m][2] = l0.z; L[m][3] = l0.w;
     L[m][4] = l1.x; L[m][5] = l1.y; L[m][6] = l1.z; L[m][7] = l1.w;
   }
 
   // ---- index chunks: a ring of P per matrix.  Every load is issued
   // unconditionally, so the wait counts are static; a chunk past the wave's
-  // range gets an offset past the buffer's range, which the range check
-  // turns into zeros without a memory access.
-  __amdgpu_buffer_rsrc_t ri[NM];
-  const uint32_t nbytes = ((N + kGiRows - 1) / kGiRows) * (uint32_t)gi64_group_bytes(K);
-#pragma unroll
-  for (int m = 0; m < NM; m++)
-    ri[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(m == 0 ? a.w : a.w2), (short)0, (int)nbytes, kBufferWord3);
-  const uint32_t vbase = gbase + kGiLutBytes + (c0 * kGiRows + lane) * kGiChunk;
+  // range, and every chunk of a lane past G, gets an offset past the
+  // buffer's range, which the range check turns into zeros without a
+  // memory access.
+  const uint32_t cstride = G * kGiChunk;  // bytes from chunk c to c + 1 of a row
+  const uint32_t vbase = live ? gbase + G * 32u + (c0 * G + lane) * kGiChunk : 0x80000000u;
   u32x4v ring[P][NM];
   auto ldc = [&](uint32_t i, u32x4v (&dst)[NM]) {
-    const uint32_t vo = i < nch ? vbase + i * (kGiRows * kGiChunk) : 0x80000000u;
+    const uint32_t vo = i < nch ? vbase + i * cstride : 0x80000000u;
 #pragma unroll
     for (int m = 0; m < NM; m++) dst[m] = __builtin_amdgcn_raw_buffer_load_b128(ri[m], vo, 0u, kNontemporal);
   };
@@ -232,7 +242,7 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
 #pragma unroll
       for (int v = 0; v < S; v++) s[m] += red[((v * NM + m) * NB + b) * 64 + lane];
     }
-    if (row < N && b < a.nb) {
+    if (live && row < N && b < a.nb) {
       if constexpr (EPI == kLprSwiglu)
         a.y[row] = swiglu_h(s[0], s[1]);
       else if constexpr (EPI == kLprPair) {
@@ -244,44 +254,45 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   }
 }
 
-// Split-block payload (LUT block then index rows) -> GI64.  One thread per
-// 16-byte piece of the GI64 block, in GI64 order: the writes are contiguous,
-// the reads 16 bytes each.  Rows past N get zero LUTs and zero indices.
-__global__ __launch_bounds__(256) void k_gi64_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
-                                                   uint32_t N, uint32_t K) {
+// Split-block payload (LUT block then index rows) -> GI with G rows per
+// group.  One thread per 16-byte piece of the GI block, in GI order: the
+// writes are contiguous, the reads 16 bytes each.  Rows past N get zero
+// LUTs and zero indices.
+__global__ __launch_bounds__(256) void k_gi_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                 uint32_t N, uint32_t K, uint32_t G) {
   const uint32_t NC = K / 32;
-  const uint32_t per_group = kGiLutBytes / 16 + NC * kGiRows;  // 16-byte pieces per group
-  const size_t total = (size_t)((N + kGiRows - 1) / kGiRows) * per_group;
+  const uint32_t per_group = 2 * G + NC * G;  // 16-byte pieces per group
+  const size_t total = (size_t)((N + G - 1) / G) * per_group;
   const uint8_t* sidx = src + (size_t)N * 32;
   for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
     const uint32_t g = (uint32_t)(t / per_group), p = (uint32_t)(t % per_group);
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (p < kGiLutBytes / 16) {  // LUT piece: row p/2, half p%2
-      const uint32_t r = g * kGiRows + p / 2;
+    if (p < 2 * G) {  // LUT piece: row p/2, half p%2
+      const uint32_t r = g * G + p / 2;
       if (r < N) v = *reinterpret_cast<const uint4*>(src + (size_t)r * 32 + (p % 2) * 16);
     } else {
-      const uint32_t q = p - kGiLutBytes / 16, c = q / kGiRows, r = g * kGiRows + q % kGiRows;
+      const uint32_t q = p - 2 * G, c = q / G, r = g * G + q % G;
       if (r < N) v = *reinterpret_cast<const uint4*>(sidx + (size_t)r * (K / 2) + (size_t)c * kGiChunk);
     }
     *reinterpret_cast<uint4*>(dst + t * 16) = v;
   }
 }
 
-// GI64 -> split-block rows: LUTs to dst_lut ([N][32] B), index rows to
+// GI -> split-block rows: LUTs to dst_lut ([N][32] B), index rows to
 // dst_idx ([N][K/2] B), for consumers that keep split-block rows (the
 // decode-step model's own weight copies).
-__global__ __launch_bounds__(256) void k_gi64_unpack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst_lut,
-                                                     uint8_t* __restrict__ dst_idx, uint32_t N, uint32_t K) {
+__global__ __launch_bounds__(256) void k_gi_unpack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst_lut,
+                                                   uint8_t* __restrict__ dst_idx, uint32_t N, uint32_t K, uint32_t G) {
   const uint32_t NC = K / 32;
   const size_t pieces = (size_t)N * (2 + NC);  // per row: 2 LUT pieces + NC chunks
   for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < pieces; t += (size_t)gridDim.x * blockDim.x) {
     const uint32_t r = (uint32_t)(t / (2 + NC)), p = (uint32_t)(t % (2 + NC));
     if (p < 2)
       *reinterpret_cast<uint4*>(dst_lut + (size_t)r * 32 + p * 16) =
-          *reinterpret_cast<const uint4*>(src + gi64_lut_offset(r, K) + p * 16);
+          *reinterpret_cast<const uint4*>(src + gi_lut_offset(G, r, K) + p * 16);
     else
       *reinterpret_cast<uint4*>(dst_idx + (size_t)r * (K / 2) + (size_t)(p - 2) * kGiChunk) =
-          *reinterpret_cast<const uint4*>(src + gi64_chunk_offset(r, p - 2, K));
+          *reinterpret_cast<const uint4*>(src + gi_chunk_offset(G, r, p - 2, K));
   }
 }
 

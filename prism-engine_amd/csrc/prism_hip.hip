@@ -45,7 +45,7 @@ struct prism_hip_ctx {
   float* scratch = nullptr;
   // Host uploads: a ring of pinned staging buffers (created on first use),
   // each with the event of the last copy out of it, and a device buffer for
-  // split-block payloads on their way to the GI64 layout.
+  // split-block payloads on their way to the GI layout.
   static constexpr int kRingSlots = 4;
   static constexpr size_t kRingSlotBytes = (size_t)16 << 20;
   void* ring[kRingSlots] = {};
@@ -66,18 +66,18 @@ static void model_detach(prism_hip_model* m);
 
 // A weight's device copy is either the split-block payload as uploaded or,
 // for 4-bit matrices the lane-per-row GEMV covers in one round of row groups,
-// the GI64 layout (gemv_lpr.hpp: the same bytes regrouped per 64 rows, each
-// group's LUTs before its index chunks).  Kernels over GI64 take the base
-// pointer as both their LUT and their index pointer.
+// the GI layout (gemv_lpr.hpp: the same bytes regrouped per group of gi
+// rows, each group's LUTs before its index chunks).  Kernels over GI take
+// the base pointer as both their LUT and their index pointer.
 struct prism_hip_weight {
   prism_hip_ctx* ctx = nullptr;
   int device = 0;
   uint32_t dim_m = 0, dim_n = 0, bits = 0, layout = 0;
   size_t bytes = 0;  // payload bytes as uploaded (split-block)
-  bool gi64 = false;
+  uint32_t gi = 0;  // GI layout: rows per group; 0: split-block
   uint8_t* d = nullptr;
   const uint8_t* lut() const { return d; }
-  const uint8_t* idx() const { return gi64 ? d : d + (size_t)dim_m * (2u << bits); }
+  const uint8_t* idx() const { return gi ? d : d + (size_t)dim_m * (2u << bits); }
 };
 
 // Split-K partials of prism_hip_gemm_dev_noalloc, the GEMM entry point that
@@ -254,18 +254,22 @@ hipStream_t pick_stream(prism_hip_ctx* ctx, void* stream) {
   return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
 }
 
-// GI64 device layout (gemv_lpr.hpp) for 4-bit matrices whose row groups
-// fill between half and all of the CUs in one round (one 64-row group per
-// workgroup; the gate/up form holds two 64 KB table sets, one workgroup per
-// CU), with rows of at least 2048 elements.  MI355X, against k_gemv_tile on
-// split-block weights: 14336 x 4096 7.2 against 8.4 us, gate + up 2 x 14336
-// x 4096 12.3 us; 4864 x 896 3.5 against 3.05 us and 896 x 4864 6.3 against
-// 3.2 us (too few groups), 2 x 18944 x 3584 19.6 against 17.6 us (two
-// rounds), so those stay split-block.
-bool gi64_layout(const prism_hip_ctx* ctx, uint32_t dm, uint32_t dn, uint32_t bits) {
-  const uint32_t groups = (dm + prism::kGiRows - 1) / prism::kGiRows;
-  return bits == 4 && dn % 64 == 0 && dn >= 2048 && 2 * groups >= (uint32_t)ctx->num_cu &&
-         groups <= (uint32_t)ctx->num_cu && prism::gi64_bytes(dm, dn) < (1ull << 31);
+// GI device layout (gemv_lpr.hpp) for 4-bit matrices with rows of at least
+// 2048 elements whose rows fill every CU in one round of groups of 32..64
+// rows (one group per workgroup; the gate/up form holds two 64 KB table
+// sets, one workgroup per CU): G = ceil(N / num_cu) rounded up to a
+// multiple of 8, so N = 14336 takes 56-row groups on 256 CUs.  Returns G, or
+// 0 for split-block.  MI355X, against k_gemv_tile on split-block weights:
+// 14336 x 4096 6.7 (64-row groups, 224 of them) against 8.4 us, gate + up
+// 2 x 14336 x 4096 12.3 us; 4864 x 896 3.5 against 3.05 us and 896 x 4864
+// 6.3 against 3.2 us (too few rows), 2 x 18944 x 3584 19.6 against 17.6 us
+// (more than 64 rows per CU: two rounds), so those stay split-block.
+uint32_t gi_rows(const prism_hip_ctx* ctx, uint32_t dm, uint32_t dn, uint32_t bits) {
+  if (bits != 4 || dn % 64 != 0 || dn < 2048) return 0;
+  const uint32_t ncu = (uint32_t)ctx->num_cu;
+  const uint32_t G = ((dm + ncu - 1) / ncu + 7) / 8 * 8;
+  if (G < 32 || G > (uint32_t)prism::kGiMaxRows || prism::gi_bytes(G, dm, dn) >= (1ull << 31)) return 0;
+  return G;
 }
 
 // ---------------------------------------------------------------- GEMV plan
@@ -493,18 +497,20 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
   return PRISM_HIP_OK;
 }
 
-// GEMV over GI64 weights (w2: gate + up, SwiGLU or with d_y2 the pair).
+// GEMV over GI weights (w2: gate + up, SwiGLU or with d_y2 the pair).
 // One or two vectors a pass: k_gemv_lpr; three or more: the matrix-core
 // kernel (K % 128 == 0) in passes of up to 16, else lane-per-row passes of
 // two.  x not 16-byte aligned: the generic kernel.
-int launch_gemv_gi64(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
-                     uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
+int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
+                   uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n;
   const bool aligned = reinterpret_cast<uintptr_t>(d_x) % 16 == 0;
-  const dim3 groups((N + prism::kGiRows - 1) / prism::kGiRows);
+  const uint32_t G = w->gi;
+  const dim3 groups((N + G - 1) / G);
   if (w2) {
     if (aligned) {
       prism::LprArgs a{};
+      a.G = G;
       a.w = w->d;
       a.w2 = w2->d;
       a.x = reinterpret_cast<const uint16_t*>(d_x);
@@ -521,6 +527,7 @@ int launch_gemv_gi64(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_
         hipLaunchKernelGGL((prism::k_gemv_lpr<16, 2, 1, prism::kLprSwiglu>), groups, dim3(1024), 0, st, a);
     } else {
       prism::GemvArgs a{};
+      a.gi = G;
       a.lut = a.idx = w->d;
       a.lut2 = a.idx2 = w2->d;
       a.x = reinterpret_cast<const uint16_t*>(d_x);
@@ -544,6 +551,7 @@ int launch_gemv_gi64(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_
     uint32_t chunk;
     if (!aligned) {
       prism::GemvArgs a{};
+      a.gi = G;
       a.lut = a.idx = w->d;
       a.x = x;
       a.y = y;
@@ -553,6 +561,7 @@ int launch_gemv_gi64(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_
       hipLaunchKernelGGL((prism::k_gemv_generic<4, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, a);
     } else if (left >= 3 && K % prism::kGmGroup == 0) {
       prism::GemvArgs a{};
+      a.gi = G;
       a.lut = a.idx = w->d;
       a.x = x;
       a.y = y;
@@ -563,6 +572,7 @@ int launch_gemv_gi64(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_
                          dim3(64 * prism::kGmWaves), 0, st, a);
     } else {
       prism::LprArgs a{};
+      a.G = G;
       a.w = w->d;
       a.x = x;
       a.y = y;
@@ -582,7 +592,7 @@ int launch_gemv_gi64(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_
 
 int launch_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
                 uint32_t nb, void* d_y, hipStream_t st, void* d_y2 = nullptr) {
-  if (w->gi64) return launch_gemv_gi64(ctx, w, w2, d_x, nb, d_y, d_y2, st);
+  if (w->gi) return launch_gemv_gi(ctx, w, w2, d_x, nb, d_y, d_y2, st);
   return launch_gemv_raw(ctx, w->bits, w->dim_m, w->dim_n, w->lut(), w->idx(), w2 ? w2->lut() : nullptr,
                          w2 ? w2->idx() : nullptr, d_x, nb, d_y, st, 0, 0.0f, nullptr, d_y2);
 }
@@ -620,7 +630,8 @@ int launch_gemm_blocks(prism_hip_ctx* ctx, const void* fn, uint32_t tiles, uint3
       HIP_TRY(ctx, hipMallocFromPoolAsync(reinterpret_cast<void**>(&P), pbytes, ctx->pool, st));
     }
   }
-  void* args[] = {&lut, &idx, &X, &Y, &M, &N, &K, &P, &kps};
+  uint32_t G = w->gi;  // GI group rows (0: split-block; k_gemm8 ignores it)
+  void* args[] = {&lut, &idx, &X, &Y, &M, &N, &K, &P, &kps, &G};
   hipError_t e = hipLaunchKernel(fn, dim3(tiles, ns), dim3(256), args, 0, st);
   if (e == hipSuccess && split) {
     const uint64_t mn = (uint64_t)M * N;
@@ -682,7 +693,7 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
     const uint32_t tiles4 = ((M + bm - 1) / bm) * ntn;
     const void* fn;
 #define PRISM_W4(MI_, SP_)                                                                   \
-  (w->gi64 ? reinterpret_cast<const void*>(&prism::k_gemm_w4<MI_, SP_, true>)                \
+  (w->gi ? reinterpret_cast<const void*>(&prism::k_gemm_w4<MI_, SP_, true>)                  \
            : reinterpret_cast<const void*>(&prism::k_gemm_w4<MI_, SP_, false>))
     if (nsplit > 1)
       fn = mi == 2 ? PRISM_W4(2, true) : mi == 4 ? PRISM_W4(4, true) : PRISM_W4(8, true);
@@ -715,8 +726,8 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
       return launch_gemm_blocks(ctx, fn, tiles8, nsteps, nsplit8, w, d_X, M, d_Y, st, fixed);
     }
   }
-  // GI64 weights (K % 64 == 0, below 2 GiB) always take k_gemm_w4 above.
-  if (w->gi64) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no GEMM kernel for this GI64 weight (%ux%u)", N, K);
+  // GI weights (K % 64 == 0, below 2 GiB) always take k_gemm_w4 above.
+  if (w->gi) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no GEMM kernel for this GI weight (%ux%u)", N, K);
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
   const uint8_t* lut = w->lut();
   const uint8_t* idx = w->idx();
@@ -739,28 +750,29 @@ int launch_decode(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, 
   const uint8_t* idx = w->idx();
   uint32_t N = w->dim_m, K = w->dim_n;
   uint16_t* out = reinterpret_cast<uint16_t*>(d_out);
-  void* args[] = {&lut, &idx, &N, &K, &row0, &nrows, &out};
+  uint32_t G = w->gi;
+  void* args[] = {&lut, &idx, &N, &K, &row0, &nrows, &out, &G};
   const void* fn = w->bits == 8 ? reinterpret_cast<const void*>(&prism::k_decode_rows<8>)
-                   : w->gi64    ? reinterpret_cast<const void*>(&prism::k_decode_rows<4, true>)
+                   : w->gi      ? reinterpret_cast<const void*>(&prism::k_decode_rows<4, true>)
                                 : reinterpret_cast<const void*>(&prism::k_decode_rows<4>);
   HIP_TRY(ctx, hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(256), args, 0, st));
   return PRISM_HIP_OK;
 }
 
 // A 4-bit weight's LUT block and index rows in split-block form at dst_lut
-// ([N][32] B) and dst_idx ([N][K/2] B), on stream st: copies, or for a GI64
+// ([N][32] B) and dst_idx ([N][K/2] B), on stream st: copies, or for a GI
 // weight the inverse regrouping.
 int copy_split_rows(prism_hip_ctx* ctx, const prism_hip_weight* w, uint8_t* dst_lut, uint8_t* dst_idx,
                     hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n;
-  if (!w->gi64) {
+  if (!w->gi) {
     HIP_TRY(ctx, hipMemcpyAsync(dst_lut, w->lut(), (size_t)N * 32, hipMemcpyDeviceToDevice, st));
     HIP_TRY(ctx, hipMemcpyAsync(dst_idx, w->idx(), (size_t)N * (K / 2), hipMemcpyDeviceToDevice, st));
     return PRISM_HIP_OK;
   }
   const size_t pieces = (size_t)N * (2 + K / 32);
   const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
-  hipLaunchKernelGGL(prism::k_gi64_unpack, dim3(grid), dim3(256), 0, st, w->d, dst_lut, dst_idx, N, K);
+  hipLaunchKernelGGL(prism::k_gi_unpack, dim3(grid), dim3(256), 0, st, w->d, dst_lut, dst_idx, N, K, w->gi);
   HIP_TRY(ctx, hipGetLastError());
   return PRISM_HIP_OK;
 }
@@ -850,7 +862,7 @@ const char* prism_hip_last_error(const prism_hip_ctx* ctx) {
 }
 
 // Host payloads go through the pinned ring (stage_h2d); device payloads
-// are copied device-to-device.  GI64 weights are regrouped on the device
+// are copied device-to-device.  GI weights are regrouped on the device
 // from a split-block copy (the context's upload buffer for host payloads).
 // `async`: return once the copies are enqueued on the context stream.
 static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool src_dev, size_t bytes, uint32_t dm,
@@ -870,7 +882,7 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
   w->bits = bits;
   w->layout = layout;
   w->bytes = bytes;
-  w->gi64 = gi64_layout(ctx, dm, dn, bits);
+  w->gi = gi_rows(ctx, dm, dn, bits);
   auto bail = [&](int rc) -> prism_hip_weight* {
     (void)rc;
     if (w->d) {
@@ -880,7 +892,7 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
     delete w;
     return nullptr;
   };
-  hipError_t e = hipMalloc(&w->d, w->gi64 ? prism::gi64_bytes(dm, dn) : bytes);
+  hipError_t e = hipMalloc(&w->d, w->gi ? prism::gi_bytes(w->gi, dm, dn) : bytes);
   if (e != hipSuccess) {
     w->d = nullptr;
     fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload (%zu bytes): hipMalloc: %s", bytes, hipGetErrorString(e));
@@ -888,7 +900,7 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
   }
   int rc = PRISM_HIP_OK;
   const void* s = src;
-  if (!w->gi64) {
+  if (!w->gi) {
     if (src_dev) {
       e = hipMemcpyAsync(w->d, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
       if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload: %s", hipGetErrorString(e));
@@ -902,12 +914,12 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
       s = ctx->d_upload;
     }
     if (rc == PRISM_HIP_OK) {
-      const size_t pieces = prism::gi64_bytes(dm, dn) / 16;
+      const size_t pieces = prism::gi_bytes(w->gi, dm, dn) / 16;
       const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
-      hipLaunchKernelGGL(prism::k_gi64_pack, dim3(grid), dim3(256), 0, ctx->stream,
-                         reinterpret_cast<const uint8_t*>(s), w->d, dm, dn);
+      hipLaunchKernelGGL(prism::k_gi_pack, dim3(grid), dim3(256), 0, ctx->stream,
+                         reinterpret_cast<const uint8_t*>(s), w->d, dm, dn, w->gi);
       e = hipGetLastError();
-      if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "GI64 pack: %s", hipGetErrorString(e));
+      if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "GI pack: %s", hipGetErrorString(e));
     }
   }
   if (rc == PRISM_HIP_OK && (!async || src_dev)) {

@@ -43,20 +43,32 @@ def _const(header: str, name: str) -> int:
 
 GW4_BN = _const("gemm_kernels.hpp", "GW4_BN")
 GW4_BK = _const("gemm_kernels.hpp", "GW4_BK")
-GI_ROWS = _const("gemv_kernels.hpp", "kGiRows")
-GI_LUT = _const("gemv_kernels.hpp", "kGiLutBytes")
+GI_MAX = _const("gemv_kernels.hpp", "kGiMaxRows")
+GI_CHUNK = _const("gemv_kernels.hpp", "kGiChunk")
 GM_TILES = _const("gemv_mfma.hpp", "kGmTiles")
 GM_ROWS = _const("gemv_mfma.hpp", "kGmRows")
 GM_WAVES = _const("gemv_mfma.hpp", "kGmWaves")
 GM_GROUP = _const("gemv_mfma.hpp", "kGmGroup")
 
 
-def gi64_group_bytes(K):
-    return GI_LUT + GI_ROWS * (K // 2)
+def gi_rows(N, K, num_cu=256):
+    """The library's layout rule (prism_hip.hip gi_rows)."""
+    if K % 64 or K < 2048:
+        return 0
+    G = (-(-N // num_cu) + 7) // 8 * 8
+    return G if 32 <= G <= GI_MAX else 0
 
 
-def gi64_bytes(N, K):
-    return -(-N // GI_ROWS) * gi64_group_bytes(K)
+def gi_group_bytes(G, K):
+    return G * 32 + G * (K // 2)
+
+
+def gi_bytes(G, N, K):
+    return -(-N // G) * gi_group_bytes(G, K)
+
+
+def gi_chunk_offset(G, r, c, K):
+    return (r // G) * gi_group_bytes(G, K) + G * 32 + (c * G + r % G) * GI_CHUNK
 
 
 def _check(voff, soff, width, num_records, alloc, what):
@@ -82,6 +94,8 @@ def _tiles(mt, nt):
 
 
 def _gemm_w4(M, N, K, MI, GI):
+    G = gi_rows(N, K) if GI else 0
+    assert not GI or G, "shape is not a GI shape"
     BM, BN, BK = 32 * MI, GW4_BN, GW4_BK
     XR = 8 * MI
     lane = np.arange(64)[:, None]
@@ -90,7 +104,7 @@ def _gemm_w4(M, N, K, MI, GI):
     its = np.arange(K // BK)[None, :]  # K steps (the scalar offset)
     mt, nt = -(-M // BM), -(-N // BN)
     x_alloc = M * K * 2
-    w_alloc = gi64_bytes(N, K) if GI else N * row_bytes
+    w_alloc = gi_bytes(G, N, K) if GI else N * row_bytes
     for t in _tiles(mt, nt):
         n0, m0 = (t % nt) * BN, (t // nt) * BM
         live = min(M - m0, BM)
@@ -107,19 +121,21 @@ def _gemm_w4(M, N, K, MI, GI):
                 ok = (xvb + soff + 16 <= (rowb + 1) * K * 2) & (xvb + soff >= rowb * K * 2)
                 assert ok[perf].all(), "an X load leaves its row"
             if GI:
-                g = (n0 + 64 * wave) // GI_ROWS
-                wv0 = g * gi64_group_bytes(K) + GI_LUT + lane * 16
-                wvs = [wv0, wv0 + 1024]
-                grp_end = (g + 1) * gi64_group_bytes(K)
+                # gemm_kernels.hpp:526-530: row 64 w + l, chunk i; rows past N past the range
+                grow = n0 + 64 * wave + lane
+                wv0 = np.where(grow < N, gi_chunk_offset(G, grow, 0, K), 0x80000000)
+                wvs = [wv0, wv0 + G * GI_CHUNK]
+                grp_end = (grow // G + 1) * gi_group_bytes(G, K)
             else:
                 rows = n0 + 64 * wave + (lane >> 1)
                 wv0 = rows * row_bytes + 16 * (lane & 1)
                 wvs = [wv0, wv0 + 32 * row_bytes]
             for i, wv in enumerate(wvs):
-                wvb, soff = np.broadcast_arrays(wv, its * (2048 if GI else 32))
+                wvb, soff = np.broadcast_arrays(wv, its * (2 * G * GI_CHUNK if GI else 32))
                 perf = _check(wvb, soff, 16, w_alloc, w_alloc, f"gemm_w4 W N={N} t={t} GI={GI}")
                 if GI:
-                    assert (wvb + soff + 16 <= grp_end)[perf].all(), "a GI64 load leaves its group"
+                    assert (wvb + soff + 16 <= np.broadcast_to(grp_end, wvb.shape))[perf].all(), \
+                        "a GI load leaves its group"
                 else:
                     r = np.broadcast_to(rows + 32 * i, wvb.shape)
                     assert not (perf & (r >= N)).any(), "a weight row past N is read"
@@ -128,7 +144,7 @@ def _gemm_w4(M, N, K, MI, GI):
 
 @pytest.mark.parametrize("M,N,K,MI,GI", [
     (2048, 14336, 4096, 8, False), (2048, 14336, 4096, 8, True),
-    (300, 9000, 2048, 4, True), (200, 2000, 2048, 8, False), (96, 2000, 2048, 4, False),
+    (300, 9100, 2048, 4, True), (64, 8192, 2048, 4, True), (200, 16384, 2048, 8, True), (200, 2000, 2048, 8, False), (96, 2000, 2048, 4, False),
     (33, 4864, 896, 2, False), (600, 4096, 1024, 8, False), (65, 4099, 1024, 2, False),
 ])
 def test_gemm_w4_offsets(M, N, K, MI, GI):
@@ -138,7 +154,7 @@ def test_gemm_w4_offsets(M, N, K, MI, GI):
 # ---- k_gemv_mfma (gemv_mfma.hpp:75-110): x rows and index groups
 @pytest.mark.parametrize("N,K,nb,bits,GI", [
     (14336, 4096, 8, 4, True), (14336, 4096, 16, 4, False), (14336, 4096, 5, 8, False),
-    (4099, 1024, 3, 4, False), (9000, 2048, 16, 4, True), (1000, 384, 4, 8, False),
+    (4099, 1024, 3, 4, False), (9100, 2048, 16, 4, True), (1000, 384, 4, 8, False),
 ])
 def test_gemv_mfma_offsets(N, K, nb, bits, GI):
     lane = np.arange(64)
@@ -146,7 +162,8 @@ def test_gemv_mfma_offsets(N, K, nb, bits, GI):
     IB = 32 * bits // 8
     ng = K // GM_GROUP
     x_alloc = nb * K * 2
-    wbytes = gi64_bytes(N, K) if GI else N * (K * bits // 8)
+    G = gi_rows(N, K) if GI else 0
+    wbytes = gi_bytes(G, N, K) if GI else N * (K * bits // 8)
     row_b = K * bits // 8
     for blk in range(-(-N // GM_ROWS)):
         n0 = blk * GM_ROWS
@@ -162,9 +179,9 @@ def test_gemv_mfma_offsets(N, K, nb, bits, GI):
                 for t in range(GM_TILES):
                     r = np.minimum(n0 + 16 * t + n, N - 1)
                     if GI:
-                        iv = (r // GI_ROWS) * gi64_group_bytes(K) + GI_LUT + (kq * GI_ROWS + r % GI_ROWS) * 16
-                        soff = k0 * 32
-                        end = (r // GI_ROWS + 1) * gi64_group_bytes(K)
+                        iv = gi_chunk_offset(G, r, kq, K)
+                        soff = k0 // 2 * G
+                        end = (r // G + 1) * gi_group_bytes(G, K)
                     else:
                         iv = r * row_b + kq * IB
                         soff = k0 * bits // 8
@@ -193,20 +210,27 @@ def test_gemv_tile_offsets_are_aligned(N, K, bits):
         assert ((vo + 4 * IW) <= (rc + 1) * row_dw * 4)[perf & live].all()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048), (16384, 2048), (8192, 2112)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (16384, 2048), (8192, 2112)])
 def test_gemv_lpr_offsets(N, K):
-    """Chunk c of wave w's range, or an offset past the range (0x80000000)."""
+    """Chunk c of wave w's range, or an offset past the range (0x80000000);
+    lanes past G always past the range (gemv_lpr.hpp:100-140)."""
+    G = gi_rows(N, K)
+    assert G
     NC = K // 32
     lane = np.arange(64)
-    nbytes = gi64_bytes(N, K)
+    nbytes = gi_bytes(G, N, K)
     for S in (8, 16):
         for w in range(S):
             c0, nch = (w * NC) // S, ((w + 1) * NC) // S - (w * NC) // S
-            for g in (0, -(-N // GI_ROWS) - 1):
-                vbase = g * gi64_group_bytes(K) + GI_LUT + (c0 * GI_ROWS + lane) * 16
+            for g in (0, -(-N // G) - 1):
+                base = g * gi_group_bytes(G, K)
+                lut = np.where(lane < G, base + lane * 32, 0x80000000)
+                for off in (0, 16):
+                    perf = _check(lut + off, 0, 16, nbytes, nbytes, "gemv_lpr LUT")
+                    assert (perf == (lane < G)).all()
+                vbase = np.where(lane < G, base + G * 32 + (c0 * G + lane) * GI_CHUNK, 0x80000000)
                 for i in range(nch + 8):  # the ring issues up to P loads past the range
-                    vo = vbase + i * 1024 if i < nch else np.full(64, 0x80000000)
+                    vo = vbase + i * G * GI_CHUNK if i < nch else np.full(64, 0x80000000)
                     perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr chunk")
-                    assert perf.all() == (i < nch)
-                    if i < nch:
-                        assert ((vo + 16) <= (g + 1) * gi64_group_bytes(K)).all()
+                    assert (perf == ((lane < G) & (i < nch))).all()
+                    assert ((vo + 16) <= base + gi_group_bytes(G, K))[perf].all()

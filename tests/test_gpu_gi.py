@@ -1,13 +1,15 @@
-"""The GI64 device layout (4-bit weights whose 64-row groups fill 128..256
-CUs with rows of >= 2048 elements, K % 64 == 0) and the two-output gate/up
-GEMV, through the C ABI against the CPU oracle.
+"""The GI device layout (4-bit weights with rows of >= 2048 elements,
+K % 64 == 0, in groups of G = 32..64 rows, G = ceil(N / num_cu) rounded up
+to a multiple of 8) and the two-output gate/up GEMV, through the C ABI
+against the CPU oracle.
 
 Every operation on a weight must give the same results whatever device
 layout the library chose for it: the lane-per-row GEMV (1..2 vectors), the
-matrix-core GEMV over GI64 (3+ vectors), the generic kernel (unaligned x),
-the GEMM, the row decode and the decode-step model's copies.  Shapes:
-14336 x 4096 (224 groups), 9000 x 2048 (141 groups, a ragged last group),
-8192 x 2112 (K % 128 != 0: no matrix-core pass), 16384 x 2048 (256 groups).
+matrix-core GEMV over GI (3+ vectors), the generic kernel (unaligned x),
+the GEMM, the row decode and the decode-step model's copies.  Shapes (on a
+256-CU MI355X): 14336 x 4096 (56-row groups, 256 of them), 9100 x 2048
+(40-row groups, 228 with a ragged last one), 8192 x 2112 (32-row groups;
+K % 128 != 0: no matrix-core pass), 16384 x 2048 (64-row groups).
 """
 import numpy as np
 import pytest
@@ -15,7 +17,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
-GI64_SHAPES = [(14336, 4096), (9000, 2048), (8192, 2112), (16384, 2048)]
+GI_SHAPES = [(14336, 4096), (9100, 2048), (8192, 2112), (16384, 2048)]
 
 
 def _rel(y, ref):
@@ -33,32 +35,35 @@ def _check(y, ref, what):
         assert err <= TOL, f"{what}: vector {b} rel err {err:.3e}"
 
 
-def _gi64(N, K, bits=4, num_cu=256):
-    groups = (N + 63) // 64
-    return bits == 4 and K % 64 == 0 and K >= 2048 and 2 * groups >= num_cu and groups <= num_cu
+def _gi(N, K, bits=4, num_cu=256):
+    """The library's layout rule (prism_hip.hip gi_rows): the group rows, or 0."""
+    if bits != 4 or K % 64 or K < 2048:
+        return 0
+    G = (-(-N // num_cu) + 7) // 8 * 8
+    return G if 32 <= G <= 64 else 0
 
 
-@pytest.mark.parametrize("N,K", GI64_SHAPES)
+@pytest.mark.parametrize("N,K", GI_SHAPES)
 @pytest.mark.parametrize("batch", [1, 2, 3, 5, 16])
-def test_gi64_gemv(pe, oracle, gpu_ctx, N, K, batch):
-    assert _gi64(N, K)
+def test_gi_gemv(pe, oracle, gpu_ctx, N, K, batch):
+    assert _gi(N, K)
     if N * K > 4 * 10**7 and batch in (3, 5):
         pytest.skip("odd batches covered at the smaller shapes")
     t = pe.synth_tensor(N, K, 4, seed=N + K + batch)
     x = pe.synth_x(batch, K, seed=batch * 3 + 1)
     w = gpu_ctx.upload_tensor(t)
-    print(f"gi64 gemv {N}x{K} batch {batch}", flush=True)
+    print(f"gi gemv {N}x{K} batch {batch}", flush=True)
     y = gpu_ctx.gemv(w, x)
     ref = oracle.gemv(x, t.payload, N, K, 4, threads=8)
-    _check(y, ref, f"GI64 {N}x{K} batch {batch}")
+    _check(y, ref, f"GI {N}x{K} batch {batch}")
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
-def test_gi64_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+def test_gi_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     """One-hot x: every output is the decoded weight itself, LUT_r[idx(r, k)],
     through the lane-per-row GEMV (one vector) and the matrix-core GEMV
-    over GI64 (six vectors at once)."""
+    over GI (six vectors at once)."""
     t = pe.synth_tensor(N, K, 4, seed=K + 11)
     lut, idx = pe.unpack_payload(t.payload, N, K, 4)
     ks = [0, 1, 31, 32, K // 2 + 5, K - 1]
@@ -76,9 +81,9 @@ def test_gi64_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
-def test_gi64_unaligned_x(pe, oracle, gpu_ctx, N, K):
-    """x not 16-byte aligned: the generic kernel reads GI64 as well."""
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+def test_gi_unaligned_x(pe, oracle, gpu_ctx, N, K):
+    """x not 16-byte aligned: the generic kernel reads GI as well."""
     import torch
     t = pe.synth_tensor(N, K, 4, seed=N - K)
     x = pe.synth_x(2, K, seed=5)
@@ -90,13 +95,13 @@ def test_gi64_unaligned_x(pe, oracle, gpu_ctx, N, K):
     gpu_ctx.gemv_dev(w, dx, 2, dy)
     torch.cuda.synchronize()
     y = dy.cpu().numpy().view(np.uint16).reshape(2, N)
-    _check(y, oracle.gemv(x, t.payload, N, K, 4, threads=8), f"GI64 {N}x{K} unaligned x")
+    _check(y, oracle.gemv(x, t.payload, N, K, 4, threads=8), f"GI {N}x{K} unaligned x")
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
-def test_gi64_decode_rows(pe, oracle, gpu_ctx, N, K):
-    """Row decode and lut_embed over GI64 are the oracle's bytes exactly,
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+def test_gi_decode_rows(pe, oracle, gpu_ctx, N, K):
+    """Row decode and lut_embed over GI are the oracle's bytes exactly,
     including rows of the ragged last group."""
     import torch
     t = pe.synth_tensor(N, K, 4, seed=3 * N + 1)
@@ -113,8 +118,8 @@ def test_gi64_decode_rows(pe, oracle, gpu_ctx, N, K):
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
-def test_gi64_upload_dev(pe, gpu_ctx, N, K):
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+def test_gi_upload_dev(pe, gpu_ctx, N, K):
     """A device-side payload is regrouped the same way as a host one."""
     import torch
     t = pe.synth_tensor(N, K, 4, seed=N * 2 + K)
@@ -129,9 +134,9 @@ def test_gi64_upload_dev(pe, gpu_ctx, N, K):
 
 # (bits, N, K): split-block shapes of every tile form (one-wave tiles, two
 # per workgroup, 8-bit), config 2's matrix, ragged K (generic kernel), and
-# GI64 shapes (the lane-per-row kernel's pair form)
+# GI shapes (the lane-per-row kernel's pair form)
 PAIR_SHAPES = [(4, 4864, 896), (4, 18944, 3584), (4, 300, 4096), (8, 300, 512), (8, 14336, 4096),
-               (4, 7, 40), (8, 9, 7), (4, 14336, 4096), (4, 9000, 2048)]
+               (4, 7, 40), (8, 9, 7), (4, 14336, 4096), (4, 9100, 2048)]
 
 
 @pytest.mark.parametrize("bits,N,K", PAIR_SHAPES)
@@ -181,30 +186,31 @@ def test_gate_up_pair_dev_and_errors(pe, gpu_ctx):
         w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9000, 2048)])
-def test_gi64_gateup_swiglu(pe, oracle, gpu_ctx, N, K):
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+def test_gi_gateup_swiglu(pe, oracle, gpu_ctx, N, K):
     tg = pe.synth_tensor(N, K, 4, seed=N + 5)
     tu = pe.synth_tensor(N, K, 4, seed=N + 6)
     x = pe.synth_x(1, K, seed=N + 7)
     wg, wu = gpu_ctx.upload_tensor(tg), gpu_ctx.upload_tensor(tu)
     y = gpu_ctx.gateup_swiglu(wg, wu, x)
     ref = oracle.gateup_swiglu(x[0], tg.payload, tu.payload, N, K, 4, threads=8)
-    _check(y, ref, f"GI64 gate_up + SwiGLU {N}x{K}")
+    _check(y, ref, f"GI gate_up + SwiGLU {N}x{K}")
     wg.free()
     wu.free()
 
 
 @pytest.mark.parametrize("M", [24, 64, 200, 300])
-def test_gi64_gemm(pe, oracle, gpu_ctx, M):
-    """Prefill GEMM over GI64 weights with a ragged last group: GEMV passes
-    (24 rows), split K (64, 200) and whole-K blocks (300); every row checked
-    against the float32 product of the decoded weights, a spread of rows
-    against the oracle."""
-    N, K = 9000, 2048
+def test_gi_gemm(pe, oracle, gpu_ctx, M):
+    """Prefill GEMM over GI weights with a ragged last group (40-row groups,
+    so a wave's 64 rows span two of them): GEMV passes (24 rows), split K
+    (64, 200) and whole-K blocks (300); every row checked against the
+    float32 product of the decoded weights, a spread of rows against the
+    oracle."""
+    N, K = 9100, 2048
     t = pe.synth_tensor(N, K, 4, seed=M + 40)
     X = pe.synth_x(M, K, seed=M + 41)
     w = gpu_ctx.upload_tensor(t)
-    print(f"gi64 gemm M={M}", flush=True)
+    print(f"gi gemm M={M}", flush=True)
     Y = gpu_ctx.gemm(w, X)
     dense = oracle.decode_rows(t.payload, N, K, 4, 0, N).view(np.float16).astype(np.float32)
     Yf = X.view(np.float16).astype(np.float32) @ dense.T
@@ -219,13 +225,13 @@ def test_gi64_gemm(pe, oracle, gpu_ctx, M):
     w.free()
 
 
-def test_gi64_model_step(pe, oracle, gpu_ctx):
+def test_gi_model_step(pe, oracle, gpu_ctx):
     """A decode-step model whose embedding (9000 x 2048) and gate/up
-    (8192 x 2048) weights were uploaded in the GI64 layout: the model's
+    (8192 x 2048) weights were uploaded in the GI layout: the model's
     split-block copies are regrouped back, and the step matches the oracle."""
     cfg = pe.Qwen2Config(n_layers=1, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64, intermediate=8192,
                          vocab=9000)
-    assert _gi64(cfg.vocab, cfg.hidden) and _gi64(cfg.intermediate, cfg.hidden)
+    assert _gi(cfg.vocab, cfg.hidden) and _gi(cfg.intermediate, cfg.hidden)
     embed, layers = pe.synth_weights(cfg, 21)
     m = pe.Model.from_tensors(gpu_ctx, cfg, embed, layers, max_seq=16)
     kv = oracle.KVState(cfg.n_layers, cfg.kv_dim, 16)
