@@ -84,6 +84,22 @@ def test_step_tiny_matches_oracle(gpu_ctx, token, pos, n_cached):
         assert np.max(np.abs(new_g - new_o)) <= 2
 
 
+@pytest.mark.parametrize("n_cached", [255, 1023, 1024, 1300])
+def test_step_long_cache_matches_oracle(gpu_ctx, n_cached):
+    """Attention splits of more than one 256-position pass: the four splits of
+    a head take ceil(sl / 4) positions each, so sl = 1024 fills exactly one
+    pass per split, sl = 1025 gives the first three splits 257 positions (a
+    second pass of one position), sl = 1301 two passes to every split."""
+    cfg = pe.Qwen2Config(**TINY)
+    m, emb_p, lay_p, kv = build(gpu_ctx, cfg, 35, n_cached, max_seq=1400)
+    print(f"long cache {n_cached}", flush=True)
+    got = m.step(11, n_cached)
+    want = oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv, 11, n_cached, threads=4)
+    err = pe.rel_err(got, want)
+    print(f"  logits rel err {err:.3e}", flush=True)
+    assert err <= STEP_TOL
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(4, 2), (4, 4), (6, 2)])
 def test_step_kv_widths_match_oracle(gpu_ctx, heads, kv_heads):
     """kv_dim 128 and 256 (up to the 256 limit) and grouped heads 3:1."""
