@@ -44,10 +44,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
-# HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 2 + WRITE_SIZE x 1,
+# HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 1.9991 + WRITE_SIZE x 1,
 # scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_lpr_hero_4bit_b1.md,
 # profiles/k_gemv_mfma_cfg4_8bit_b8.md
-PMC_TRAFFIC = {("hero", 1): 30088192, ("cfg4", 8): 67160340}
+PMC_TRAFFIC = {("hero", 1): 30073588, ("cfg4", 8): 67160340}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
