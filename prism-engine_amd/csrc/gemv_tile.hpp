@@ -94,8 +94,8 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
 //  kEpiAttnIn x is the attention output of the decode step, given as the
 //            split partials of k_step_attention (a.xpart, [K/64 heads]
 //            [kAttnSplits][2 + 64] fp32): each thread combines its own units
-//            (head u/8, dims 8*(u%8)..+7) and rounds them to fp16, the value
-//            k_step_attn_combine would store.
+//            (head u/8, dims 8*(u%8)..+7) and rounds them to fp16: the
+//            attention output of attention_cpu (evaluator.rs:104-146).
 //  kEpiPair  DUAL only: instead of the SwiGLU epilogue, the raw gate and up
 //            outputs y[row] = f16(gate), y2[row] = f16(up) (the outputs of
 //            templates/fused_gate_up.metal:16-97; the CPU path computes them

@@ -13,7 +13,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-# (N, K, bits): GI64 (hero), split-block 4-bit, 8-bit, a payload of many ring
+# (N, K, bits): GI (hero, 56-row groups), split-block 4-bit, 8-bit, a payload of many ring
 # slots, and tiny/ragged ones
 SHAPES = [(14336, 4096, 4), (4864, 896, 4), (1000, 2048, 8), (18944, 3584, 4), (3, 100, 4), (7, 24, 8)]
 

@@ -13,7 +13,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 # (bits, N, K, M first call, M second call): split-K 4-bit (4 and 2 splits),
-# GI64 and split-block device layouts, split-K 8-bit, an unsplit prefill and
+# GI and split-block device layouts, split-K 8-bit, an unsplit prefill and
 # the GEMV path (no partials at all).
 CASES = [
     (4, 14336, 4096, 256, 64),
