@@ -45,7 +45,7 @@
 //    back to waiting for every load.
 //  * The S wave partials of each row are added in LDS in wave order and
 //    rounded once.
-// Requires K % 64 == 0, 64-byte aligned x rows (scalar loads of 16 dwords)
+// Requires K % 64 == 0, 16-byte aligned x (scalar loads need dword alignment)
 // and the weight block below 2 GiB (32-bit buffer offsets; each offset, row
 // and chunk included, is the per-lane VGPR offset, which the range check
 // covers).

@@ -81,6 +81,35 @@ def test_gi_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     w.free()
 
 
+@pytest.mark.parametrize("nb", [1, 2])
+def test_gi_lpr_x_on_16_byte_boundary(pe, oracle, gpu_ctx, nb):
+    """x 16-byte aligned but not 64-byte aligned: the lane-per-row kernel
+    reads x with scalar loads, which need dword alignment only."""
+    import torch
+    N, K = 14336, 4096
+    t = pe.synth_tensor(N, K, 4, seed=77)
+    x = pe.synth_x(nb, K, seed=78)
+    w = gpu_ctx.upload_tensor(t)
+    buf = torch.zeros(nb * K + 64, dtype=torch.int16, device="cuda")
+    assert buf.data_ptr() % 64 == 0
+    buf[8:8 + nb * K] = torch.from_numpy(x.reshape(-1).view(np.int16)).cuda()
+    dx = buf[8:]  # 16 bytes past a 64-byte boundary
+    dy = torch.empty(nb * N, dtype=torch.int16, device="cuda")
+    print(f"LPR x at +16 B, nb={nb}", flush=True)
+    gpu_ctx.gemv_dev(w, dx, nb, dy)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy().view(np.uint16).reshape(nb, N)
+    want = oracle.gemv(x, t.payload, N, K, 4, threads=8)
+    _check(y, want, f"GI LPR x at +16 B nb={nb}")
+    # the same call on 64-byte-aligned x gives the same bits
+    dx2 = torch.from_numpy(x.reshape(-1).view(np.int16)).cuda()
+    dy2 = torch.empty(nb * N, dtype=torch.int16, device="cuda")
+    gpu_ctx.gemv_dev(w, dx2, nb, dy2)
+    torch.cuda.synchronize()
+    assert np.array_equal(dy2.cpu().numpy().view(np.uint16).reshape(nb, N), y)
+    w.free()
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
 def test_gi_unaligned_x(pe, oracle, gpu_ctx, N, K):
     """x not 16-byte aligned: the generic kernel reads GI as well."""
