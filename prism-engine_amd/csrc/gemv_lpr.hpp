@@ -34,13 +34,15 @@
 //    half its LDS cycles to conflicts).  One v_perm builds the address
 //    (lane*4 in byte 0, the index byte in byte 1) and one ds_read_b32 reads
 //    the pair: per element one VALU op and half an LDS read, plus the v_dot2.
-//  * Loads: the LUTs (two 16-byte loads per lane), the first P chunks per
-//    wave and the first x block go out first; after the table build each
-//    wave keeps P chunk loads in flight, so the index stream is requested
-//    at the rate the lookups consume it (with every chunk requested up
-//    front, the waves whose chunks return last decode all of theirs at the
-//    end; with 8 in flight the hero shape also ran slower).  Chunk loads are
-//    unconditional (past the wave's range they read zeros through the range
+//  * Loads: the LUTs (two 16-byte loads per lane), the first chunks of each
+//    wave (kLprFirst when the wave's chunk count is a compile-time constant,
+//    else one x block's worth) and the first x block go out first; after
+//    the table build each wave keeps a fixed number of chunk loads ahead of
+//    its lookups (kLprAhead, or one x block), so the index stream is
+//    requested at the rate the lookups consume it (with every chunk
+//    requested up front, the waves whose chunks return last decode all of
+//    theirs at the end).  Chunk loads are unconditional or statically
+//    conditional (past the wave's range they read zeros through the range
 //    check), so the compiler's wait counts stay exact instead of falling
 //    back to waiting for every load.
 //  * The S wave partials of each row are added in LDS in wave order and
@@ -65,6 +67,17 @@ constexpr int kLprPlain = 0;   // y[b][row] = f16(acc)
 constexpr int kLprSwiglu = 1;  // NM = 2: y[row] = swiglu(f16(gate), f16(up))
 constexpr int kLprPair = 2;    // NM = 2: y[row] = f16(gate), y2[row] = f16(up)
 
+// Chunk loads of a wave whose chunk count is a compile-time constant (NCH):
+// kLprFirst requested before the table build, then kLprAhead ahead of the
+// chunk being looked up (the first kLprFirst - kLprAhead chunks request
+// nothing).  Hero shape, MI355X, one box, three runs each: 6.59-6.60 us
+// against 6.88-6.91 for the run-time loop with 4 in flight; (first, ahead) =
+// (4, 4) 6.72-6.77, (8, 4) 6.62-6.67, (10, 4) 6.96-6.99, (12, 4) 7.41,
+// (16, -) 8.17.  The straight-line sequence is part of the gain: (4, 4)
+// unrolled beats the loop.
+constexpr int kLprFirst = 6;
+constexpr int kLprAhead = 5;
+
 struct LprArgs {
   const uint8_t* w;    // GI weights
   const uint8_t* w2;   // NM = 2: up matrix, same shape
@@ -77,16 +90,21 @@ struct LprArgs {
   uint32_t G;          // rows per group (<= 64)
 };
 
-template <int S, int NM, int NB, int EPI>
+template <int S, int NM, int NB, int EPI, int NCH = 0>
 __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   static_assert(S == 4 || S == 8 || S == 16, "waves per group");
   static_assert(NM == 1 || NM == 2, "one matrix or gate + up");
   static_assert(NB == 1 || NB == 2, "batch vectors per pass");
   static_assert(EPI == kLprPlain || (NM == 2 && NB == 1), "gate/up epilogues are single-vector");
-  // x chunks per scalar block (16 SGPRs per chunk and vector) and chunk
-  // loads in flight per wave (a ring of P slots, refilled in order)
+  // x chunks per scalar block (16 SGPRs per chunk and vector).  Chunk loads:
+  // a ring of R slots (chunk c in slot c % R), chunk c + DR requested once
+  // chunk c's table addresses are formed.  NCH = 0 (chunks per wave known at
+  // run time): R = DR = XB, a loop over x blocks; NCH > 0 (the host launches
+  // it only when the wave's chunk count is NCH): kLprFirst / kLprAhead, one
+  // straight-line sequence.
   constexpr int XB = (NM == 1 && NB == 1) ? 4 : 2;
-  constexpr int P = XB;
+  constexpr int R = NCH == 0 ? XB : (NCH < kLprFirst ? NCH : kLprFirst);
+  constexpr int DR = NCH == 0 ? XB : (R < kLprAhead ? R : kLprAhead);
   constexpr int LO = 16 / S;  // low nibbles of the table entries a thread builds
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
   typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
@@ -134,14 +152,14 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   // memory access.
   const uint32_t cstride = G * kGiChunk;  // bytes from chunk c to c + 1 of a row
   const uint32_t vbase = live ? gbase + G * 32u + (c0 * G + lane) * kGiChunk : 0x80000000u;
-  u32x4v ring[P][NM];
+  u32x4v ring[R][NM];
   auto ldc = [&](uint32_t i, u32x4v (&dst)[NM]) {
     const uint32_t vo = i < nch ? vbase + i * cstride : 0x80000000u;
 #pragma unroll
     for (int m = 0; m < NM; m++) dst[m] = __builtin_amdgcn_raw_buffer_load_b128(ri[m], vo, 0u, kNontemporal);
   };
 #pragma unroll
-  for (int u = 0; u < P; u++) ldc(u, ring[u]);
+  for (int u = 0; u < R; u++) ldc(u, ring[u]);
 
   // ---- first x block (scalar loads; x rows are read past the wave's range
   // only inside the row, so no guard is needed for them)
@@ -185,46 +203,55 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- lookups and products.  Chunk i + u uses ring slot u and x block
-  // entry u; its slot is refilled with chunk i + u + P once its table
-  // addresses are formed.  Full blocks of XB chunks run without branches;
-  // the last partial block skips its missing chunks.
+  // ---- lookups and products.  Chunk c uses ring slot `slot` and x block
+  // entry `xu`; with `refill`, chunk c + DR is requested into its slot once
+  // chunk c's table addresses are formed.
   const uint32_t lanebase = lane * 4u;
   float acc[NM][NB][2];
 #pragma unroll
   for (int m = 0; m < NM; m++)
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[m][b][0] = acc[m][b][1] = 0.0f;
-  auto chunk = [&](uint32_t c, int u) {
+  auto chunk = [&](uint32_t c, int slot, int xu, bool refill) {
     uint32_t pr[NM][16];
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
       for (int j = 0; j < 16; j++) {
-        const uint32_t ad = __builtin_amdgcn_perm(ring[u][m][j >> 2], lanebase, 0x0C0C0000u | ((4u + (j & 3)) << 8));
+        const uint32_t ad = __builtin_amdgcn_perm(ring[slot][m][j >> 2], lanebase, 0x0C0C0000u | ((4u + (j & 3)) << 8));
         pr[m][j] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds + m * kLprTableDw) + ad);
       }
-    ldc(c + P, ring[u]);
+    if (refill) ldc(c + DR, ring[(slot + DR) % R]);
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
       for (int b = 0; b < NB; b++)
 #pragma unroll
-        for (int j = 0; j < 16; j++) acc[m][b][j & 1] = dot2(pr[m][j], xs[b][u][j], acc[m][b][j & 1]);
+        for (int j = 0; j < 16; j++) acc[m][b][j & 1] = dot2(pr[m][j], xs[b][xu][j], acc[m][b][j & 1]);
     __builtin_amdgcn_sched_barrier(0);
   };
-  const uint32_t nfull = nch / XB;
-  uint32_t i = 0;
-  for (uint32_t it = 0; it < nfull; it++, i += XB) {
-    if (it != 0) ldx(i);
+  if constexpr (NCH > 0) {
 #pragma unroll
-    for (int u = 0; u < XB; u++) chunk(i + u, u);
-  }
-  if (i < nch) {
-    if (i != 0) ldx(i);
+    for (int c = 0; c < NCH; c++) {
+      if (c % XB == 0 && c != 0) ldx(c);
+      chunk(c, c % R, c % XB, c >= R - DR && c + DR < NCH);
+    }
+  } else {
+    // full blocks of XB chunks run without branches; the last partial block
+    // skips its missing chunks
+    const uint32_t nfull = nch / XB;
+    uint32_t i = 0;
+    for (uint32_t it = 0; it < nfull; it++, i += XB) {
+      if (it != 0) ldx(i);
 #pragma unroll
-    for (int u = 0; u < XB - 1; u++)
-      if (i + u < nch) chunk(i + u, u);
+      for (int u = 0; u < XB; u++) chunk(i + u, u, u, true);
+    }
+    if (i < nch) {
+      if (i != 0) ldx(i);
+#pragma unroll
+      for (int u = 0; u < XB - 1; u++)
+        if (i + u < nch) chunk(i + u, u, u, true);
+    }
   }
 
   // ---- wave partials -> LDS -> rows (waves 0 .. NB-1 finish one vector each)

@@ -501,6 +501,21 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
 // One or two vectors a pass: k_gemv_lpr; three or more: the matrix-core
 // kernel (K % 128 == 0) in passes of up to 16, else lane-per-row passes of
 // two.  x not 16-byte aligned: the generic kernel.
+// k_gemv_lpr with the wave's chunk count as a compile-time constant when
+// every wave has the same count (K/32 a multiple of S) and it is 8 or 16,
+// else the run-time loop.
+template <int S, int NM, int NB, int EPI>
+void launch_lpr(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
+  const uint32_t NC = a.K / 32;
+  const uint32_t nch = NC % S == 0 ? NC / S : 0;
+  if (nch == 16)
+    hipLaunchKernelGGL((prism::k_gemv_lpr<S, NM, NB, EPI, 16>), groups, dim3(64 * S), 0, st, a);
+  else if (nch == 8)
+    hipLaunchKernelGGL((prism::k_gemv_lpr<S, NM, NB, EPI, 8>), groups, dim3(64 * S), 0, st, a);
+  else
+    hipLaunchKernelGGL((prism::k_gemv_lpr<S, NM, NB, EPI>), groups, dim3(64 * S), 0, st, a);
+}
+
 int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
                    uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n;
@@ -522,9 +537,9 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       // the pair form splits K over the waves as the one-matrix GEMV does
       // (8 waves), so each output is that GEMV's bit for bit
       if (d_y2)
-        hipLaunchKernelGGL((prism::k_gemv_lpr<8, 2, 1, prism::kLprPair>), groups, dim3(512), 0, st, a);
+        launch_lpr<8, 2, 1, prism::kLprPair>(groups, st, a);
       else
-        hipLaunchKernelGGL((prism::k_gemv_lpr<16, 2, 1, prism::kLprSwiglu>), groups, dim3(1024), 0, st, a);
+        launch_lpr<16, 2, 1, prism::kLprSwiglu>(groups, st, a);
     } else {
       prism::GemvArgs a{};
       a.gi = G;
@@ -580,9 +595,9 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.K = K;
       a.nb = chunk = left >= 2 ? 2u : 1u;
       if (chunk == 2)
-        hipLaunchKernelGGL((prism::k_gemv_lpr<8, 1, 2, prism::kLprPlain>), groups, dim3(512), 0, st, a);
+        launch_lpr<8, 1, 2, prism::kLprPlain>(groups, st, a);
       else
-        hipLaunchKernelGGL((prism::k_gemv_lpr<8, 1, 1, prism::kLprPlain>), groups, dim3(512), 0, st, a);
+        launch_lpr<8, 1, 1, prism::kLprPlain>(groups, st, a);
     }
     HIP_TRY(ctx, hipGetLastError());
     b0 += chunk;
