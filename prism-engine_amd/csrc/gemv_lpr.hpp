@@ -70,13 +70,17 @@ constexpr int kLprPair = 2;    // NM = 2: y[row] = f16(gate), y2[row] = f16(up)
 // Chunk loads of a wave whose chunk count is a compile-time constant (NCH):
 // kLprFirst requested before the table build, then kLprAhead ahead of the
 // chunk being looked up (the first kLprFirst - kLprAhead chunks request
-// nothing).  Hero shape, MI355X, one box, three runs each: 6.59-6.60 us
-// against 6.88-6.91 for the run-time loop with 4 in flight; (first, ahead) =
-// (4, 4) 6.72-6.77, (8, 4) 6.62-6.67, (10, 4) 6.96-6.99, (12, 4) 7.41,
-// (16, -) 8.17.  The straight-line sequence is part of the gain: (4, 4)
-// unrolled beats the loop.
-constexpr int kLprFirst = 6;
+// nothing), with x in scalar blocks of kLprXBlock chunks.  Hero shape,
+// MI355X, timing copies on one box: x blocks of 4 chunks, (first, ahead) =
+// (6, 5) 6.59-6.60 us against 6.88-6.91 for the run-time loop with 4 in
+// flight; (4, 4) 6.72-6.77, (8, 4) 6.62-6.67, (10, 4) 6.96-6.99, (12, 4)
+// 7.41, everything first 8.17; x blocks of 2 chunks on another box: (5, 5)
+// 6.49-6.65 and (4, 4) 6.52-6.60 against 6.62-6.68 for (6, 5) with blocks of
+// 4; blocks of 1 or 8, or double-buffered x, were slower.  The
+// straight-line sequence is part of the gain: (4, 4) unrolled beats the loop.
+constexpr int kLprFirst = 5;
 constexpr int kLprAhead = 5;
+constexpr int kLprXBlock = 2;
 
 struct LprArgs {
   const uint8_t* w;    // GI weights
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   // run time): R = DR = XB, a loop over x blocks; NCH > 0 (the host launches
   // it only when the wave's chunk count is NCH): kLprFirst / kLprAhead, one
   // straight-line sequence.
-  constexpr int XB = (NM == 1 && NB == 1) ? 4 : 2;
+  constexpr int XB = NCH > 0 ? kLprXBlock : (NM == 1 && NB == 1) ? 4 : 2;
   constexpr int R = NCH == 0 ? XB : (NCH < kLprFirst ? NCH : kLprFirst);
   constexpr int DR = NCH == 0 ? XB : (R < kLprAhead ? R : kLprAhead);
   constexpr int LO = 16 / S;  // low nibbles of the table entries a thread builds
