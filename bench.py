@@ -47,7 +47,7 @@ MALL_BYTES = 256 << 20
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 1.9991 + WRITE_SIZE x 1,
 # scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_lpr_hero_4bit_b1.md,
 # profiles/k_gemv_mfma_cfg4_8bit_b8.md
-PMC_TRAFFIC = {("hero", 1): 30073588, ("cfg4", 8): 67185610}
+PMC_TRAFFIC = {("hero", 1): 30113277, ("cfg4", 8): 67185610}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
