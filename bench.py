@@ -45,9 +45,8 @@ HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 1.9991 + WRITE_SIZE x 1,
-# scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_lpr_hero_4bit_b1.md,
-# profiles/k_gemv_mfma_cfg4_8bit_b8.md
-PMC_TRAFFIC = {("hero", 1): 30113277, ("cfg4", 8): 67185610}
+# scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_lpr_hero_4bit_b1.md
+PMC_TRAFFIC = {("hero", 1): 30113277}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
@@ -84,11 +83,11 @@ def cpu_model() -> str:
 
 
 def gi_rows(bits: int, N: int, K: int, num_cu: int) -> int:
-    """The library's device-layout rule (prism_hip.hip gi_rows): 4-bit
-    matrices with K % 64 == 0 and K >= 2048 whose rows fill every CU in one
-    round of 32..64-row groups are regrouped to the GI layout (G rows per
-    group) and run on the lane-per-row GEMV.  Returns G, or 0."""
-    if bits != 4 or K % 64 or K < 2048:
+    """The library's device-layout rule (prism_hip.hip gi_rows): matrices
+    with K >= 2048 (4-bit: K % 64 == 0; 8-bit: K % 512 == 0) whose rows fill
+    every CU in one round of 32..64-row groups are regrouped to the GI layout
+    (G rows per group) and run on the lane-per-row GEMVs.  Returns G, or 0."""
+    if K < 2048 or bits not in (4, 8) or K % (64 if bits == 4 else 512):
         return 0
     G = (-(-N // num_cu) + 7) // 8 * 8
     return G if 32 <= G <= 64 else 0
@@ -644,16 +643,23 @@ def main() -> int:
         sk = min(4, 256 // blocks, (K // 64) // 8)
         if sk >= 2:
             gemm4 = f"k_gemm_w4<{smi}>{gtag} in {sk} K splits + k_gemm_split_sum"
-    if gi:
+    lpr8_static = (K // 128) in (16, 32, 64)
+    if gi and bits == 8:
+        nbp = 1 if batch == 1 else 2 if batch == 2 else 4 if batch <= 4 else 8
+        gemv_name = (f"k_gemv_lpr8<8,1,{nbp}>{gtag}" if batch <= (8 if lpr8_static else 4) else
+                     f"k_gemv_mfma<8,GI>{gtag}")
+    elif gi:
         gemv_name = (f"k_gemv_lpr<8,1,{batch}>{gtag}" if batch <= 2 else
                      f"k_gemv_mfma<4,GI>{gtag}" if K % 128 == 0 else f"k_gemv_lpr<8,1,2> passes{gtag}")
     else:
         gemv_name = f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile"
     kernel_name = {"floor": "k_stream_read", "gemv": gemv_name,
-                   "gateup": f"k_gemv_lpr<16,2,1,SwiGLU>{gtag}" if gi else "k_gemv_tile (DUAL gate_up + SwiGLU)",
+                   "gateup": ((f"k_gemv_lpr8<8,2,1,SwiGLU>{gtag}" if bits == 8 else f"k_gemv_lpr<16,2,1,SwiGLU>{gtag}")
+                              if gi else "k_gemv_tile (DUAL gate_up + SwiGLU)"),
                    "gemm": ("GEMV passes" if batch <= (48 if bits == 8 else 32) else
                             gemm4 if bits == 4 else
-                            "k_gemm8" if batch > 256 and K % 64 == 0 else
+                            f"k_gemm8{gtag}" if (batch > 256 or gi) and K % 64 == 0 and
+                            not (batch <= 256 and min(4, 256 // -(-N // 128), (K // 64) // 8) >= 2) else
                             f"k_gemm8 in {min(4, 256 // -(-N // 128), (K // 64) // 8)} K splits + k_gemm_split_sum"
                             if K % 64 == 0 and min(4, 256 // -(-N // 128), (K // 64) // 8) >= 2 else "k_gemm<8>")}[kind]
     roof["kernel"] = kernel_name

@@ -205,11 +205,14 @@ constexpr int GM8_BK = 64;
 
 // SPLIT: block (x, y) covers K steps [y kps, min(K / 64, (y + 1) kps)) and
 // writes its fp32 partial tile to part[y][M][N], as k_gemm_w4<MI, true> does.
-template <bool SPLIT>
+// GI: the weights are in the GI layout with G rows per group (gemv_lpr.hpp;
+// lut and idx both point at it); a thread's 16 index bytes of a K step are
+// one chunk of its row.
+template <bool SPLIT, bool GI = false>
 __global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, const uint8_t* __restrict__ idx,
                                                const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, uint32_t M,
                                                uint32_t N, uint32_t K, float* __restrict__ part, uint32_t kps,
-                                               uint32_t /* G: the GI layout's group rows, 4-bit only */) {
+                                               uint32_t G) {
   constexpr int BM = GM8_BM, BN = GM8_BN, BK = GM8_BK, P = BK + 8;
   constexpr int XU = BM * BK / 8 / 256;  // 16-byte X chunks per thread per step (8)
   constexpr int WU = BN * BK / 16 / 256; // 16-byte index chunks per thread per step (2)
@@ -239,14 +242,26 @@ __global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, 
   // ---- LUTs of this block's rows -> LDS (rows past N are zero)
   {
     constexpr int U4 = BN * 256 * 2 / 16;
-    const uint4* src = reinterpret_cast<const uint4*>(lut + (size_t)n0 * 512);
     uint4* dst = reinterpret_cast<uint4*>(sL);
     const uint32_t live_u4 = (N - n0 < (uint32_t)BN ? N - n0 : (uint32_t)BN) * 32;
-    for (int i = tid; i < U4; i += 256) dst[i] = (uint32_t)i < live_u4 ? src[i] : make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < U4; i += 256) {
+      // piece i % 32 of row n0 + i / 32 (GI: the block's rows may span groups)
+      const uint32_t r = n0 + (uint32_t)i / 32;
+      const uint4* src =
+          reinterpret_cast<const uint4*>(lut + (GI ? gi_lut_offset(G, r, K, 8) : (size_t)r * 512) + 16 * (i % 32));
+      dst[i] = (uint32_t)i < live_u4 ? *src : make_uint4(0, 0, 0, 0);
+    }
   }
 
   // chunk c = tid + 256 i: X row c / 8, column chunk c % 8; index row c / 4, chunk c % 4
   uint4 ra[XU], rb[WU];
+  // GI: byte offset of chunk 0 of each of the thread's index rows
+  size_t wrow[WU];
+#pragma unroll
+  for (int i = 0; i < WU; i++) {
+    const uint32_t n = n0 + ((tid + 256 * i) >> 2);
+    wrow[i] = GI ? gi_chunk_offset(G, n < N ? n : 0u, 0, K, 8) : (size_t)n * K;
+  }
   auto gload = [&](uint32_t k0) {
 #pragma unroll
     for (int i = 0; i < XU; i++) {
@@ -258,8 +273,8 @@ __global__ __launch_bounds__(256) void k_gemm8(const uint8_t* __restrict__ lut, 
     for (int i = 0; i < WU; i++) {
       const int c = tid + 256 * i;
       const uint32_t n = n0 + (c >> 2);
-      rb[i] = (n < N) ? *reinterpret_cast<const uint4*>(idx + (size_t)n * K + k0 + 16 * (c & 3))
-                      : make_uint4(0, 0, 0, 0);
+      const size_t off = GI ? wrow[i] + (size_t)(k0 / 16 + (c & 3)) * G * 16 : wrow[i] + k0 + 16 * (c & 3);
+      rb[i] = (n < N) ? *reinterpret_cast<const uint4*>(idx + off) : make_uint4(0, 0, 0, 0);
     }
   };
   auto lstore = [&]() {
@@ -506,7 +521,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   for (int s = 0; s < 2; s++) {
     uint32_t n = n0 + 64 * wave + 32 * s + j;
     n = n < N ? n : N - 1;
-    const uint4* lr = reinterpret_cast<const uint4*>(lut + (GI ? gi_lut_offset(G, n, K) : (size_t)n * 32));
+    const uint4* lr = reinterpret_cast<const uint4*>(lut + (GI ? gi_lut_offset(G, n, K, 4) : (size_t)n * 32));
     pl[s] = make_planes(lr[0], lr[1]);
   }
   // ---- DMA sources; reads past the descriptors' ranges return 0
@@ -514,7 +529,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(X + (size_t)m0 * K), (short)0, (int)(live * K * 2u), kGwdWord3);
   const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)idx, (short)0, (int)(GI ? (uint32_t)gi_bytes(G, N, K) : N * row_bytes), kGwdWord3);
+      (void*)idx, (short)0, (int)(GI ? (uint32_t)gi_bytes(G, N, K, 4) : N * row_bytes), kGwdWord3);
   const uint32_t lr8 = (uint32_t)lane >> 3, lc = ((uint32_t)lane & 7u) ^ lr8;
   // Per-lane VGPR offsets of each DMA instruction (row and chunk); the
   // scalar offset carries only the K step.
@@ -525,7 +540,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
   // GI: instruction i reads chunk 2 (it + kb) + i of row 64 w + l (rows past
   // N get an offset past the range: zeros); a K step moves 2 chunks
   const uint32_t grow = n0 + 64u * wave + (uint32_t)lane;
-  const uint32_t wv0 = GI ? (grow < N ? (uint32_t)gi_chunk_offset(G, grow, 0, K) : 0x80000000u)
+  const uint32_t wv0 = GI ? (grow < N ? (uint32_t)gi_chunk_offset(G, grow, 0, K, 4) : 0x80000000u)
                           : (n0 + 64u * wave + ((uint32_t)lane >> 1)) * row_bytes + 16u * ((uint32_t)lane & 1u);
   const uint32_t wv[2] = {wv0, GI ? wv0 + G * (uint32_t)kGiChunk : wv0 + 32u * row_bytes};
 

@@ -65,35 +65,41 @@ struct GemvArgs {
 // unaligned x): one wave per row, element-strided.  Follows lut_gemv_cpu's
 // ragged-K rule for 4-bit weights: row stride K/2 bytes, only the first
 // (K/8)*8 elements contribute.
-// GI: the group-interleaved 4-bit device layout (k_gemv_lpr, gemv_lpr.hpp,
-// describes it): ceil(N/G) groups of [G x 32 B LUTs][K/32 chunks][G
-// rows][16 B], rows past N zero, G <= kGiMaxRows rows per group (one per
-// lane of a wave).
+// GI: the group-interleaved device layout (gemv_lpr.hpp describes it), for
+// 4- and 8-bit weights: ceil(N/G) groups of [G row LUTs (32 B at 4 bits,
+// 512 B at 8)][row bytes / 16 chunks][G rows][16 B], rows past N zero,
+// G <= kGiMaxRows rows per group (one per lane of a wave).  A chunk holds 32
+// elements at 4 bits, 16 at 8.
 constexpr int kGiMaxRows = 64;  // rows per group at most
-constexpr int kGiChunk = 16;    // index bytes per chunk (32 elements)
+constexpr int kGiChunk = 16;    // index bytes per chunk
 
-__host__ __device__ __forceinline__ size_t gi_group_bytes(uint32_t G, uint32_t K) {
-  return (size_t)G * 32 + (size_t)G * (K / 2);
+__host__ __device__ __forceinline__ uint32_t gi_lut_bytes(uint32_t bits) { return 2u << bits; }
+__host__ __device__ __forceinline__ size_t gi_group_bytes(uint32_t G, uint32_t K, uint32_t bits) {
+  return (size_t)G * gi_lut_bytes(bits) + (size_t)G * (K * bits / 8);
 }
-__host__ __device__ __forceinline__ size_t gi_bytes(uint32_t G, uint32_t N, uint32_t K) {
-  return (size_t)((N + G - 1) / G) * gi_group_bytes(G, K);
+__host__ __device__ __forceinline__ size_t gi_bytes(uint32_t G, uint32_t N, uint32_t K, uint32_t bits) {
+  return (size_t)((N + G - 1) / G) * gi_group_bytes(G, K, bits);
 }
 // Byte offset of row r's LUT, of its chunk c, and of the byte holding its
 // element k.
-__host__ __device__ __forceinline__ size_t gi_lut_offset(uint32_t G, uint32_t r, uint32_t K) {
-  return (size_t)(r / G) * gi_group_bytes(G, K) + (size_t)(r % G) * 32;
+__host__ __device__ __forceinline__ size_t gi_lut_offset(uint32_t G, uint32_t r, uint32_t K, uint32_t bits) {
+  return (size_t)(r / G) * gi_group_bytes(G, K, bits) + (size_t)(r % G) * gi_lut_bytes(bits);
 }
-__host__ __device__ __forceinline__ size_t gi_chunk_offset(uint32_t G, uint32_t r, uint32_t c, uint32_t K) {
-  return (size_t)(r / G) * gi_group_bytes(G, K) + (size_t)G * 32 + ((size_t)c * G + (r % G)) * kGiChunk;
+__host__ __device__ __forceinline__ size_t gi_chunk_offset(uint32_t G, uint32_t r, uint32_t c, uint32_t K,
+                                                           uint32_t bits) {
+  return (size_t)(r / G) * gi_group_bytes(G, K, bits) + (size_t)G * gi_lut_bytes(bits) +
+         ((size_t)c * G + (r % G)) * kGiChunk;
 }
-__host__ __device__ __forceinline__ size_t gi_index_at(uint32_t G, uint32_t r, uint32_t k, uint32_t K) {
-  return gi_chunk_offset(G, r, k / 32, K) + (k % 32) / 2;
+__host__ __device__ __forceinline__ size_t gi_index_at(uint32_t G, uint32_t r, uint32_t k, uint32_t K,
+                                                       uint32_t bits) {
+  const uint32_t per = 128 / bits;  // elements per chunk
+  return gi_chunk_offset(G, r, k / per, K, bits) + (k % per) * bits / 8;
 }
 
 // MODE: kGenSingle, or gate + up rows (lut2/idx2) with the SwiGLU
 // epilogue (kGenSwiglu) or the two raw outputs y, y2 (kGenPair).
-// GI: 4-bit weights in the GI layout with a.gi rows per group (a.lut and
-// a.idx both point at it).
+// GI: weights in the GI layout with a.gi rows per group (a.lut and a.idx
+// both point at it).
 constexpr int kGenSingle = 0, kGenSwiglu = 1, kGenPair = 2;
 template <int BITS, int MODE, bool GI = false>
 __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
@@ -108,16 +114,17 @@ __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
   for (uint32_t b = 0; b < nb; b++) {
     float acc[NM];
     for (int m = 0; m < NM; m++) {
-      const uint8_t* lut = (m == 0 ? a.lut : a.lut2) + (GI ? gi_lut_offset(a.gi, row, K) : (size_t)row * (2u << BITS));
+      const uint8_t* lut =
+          (m == 0 ? a.lut : a.lut2) + (GI ? gi_lut_offset(a.gi, row, K, BITS) : (size_t)row * (2u << BITS));
       const uint8_t* idx = (m == 0 ? a.idx : a.idx2) + (GI ? 0 : (size_t)row * stride);
       float s = 0.0f;
       for (uint32_t k = lane; k < keff; k += 64) {
         uint32_t e;
         if (BITS == 4) {
-          const uint8_t byte = GI ? idx[gi_index_at(a.gi, row, k, K)] : idx[k >> 1];
+          const uint8_t byte = GI ? idx[gi_index_at(a.gi, row, k, K, 4)] : idx[k >> 1];
           e = (k & 1) ? (byte >> 4) : (byte & 15u);
         } else {
-          e = idx[k];
+          e = GI ? idx[gi_index_at(a.gi, row, k, K, 8)] : idx[k];
         }
         const uint16_t lv = (uint16_t)(lut[2 * e] | (lut[2 * e + 1] << 8));
         s += h2f(a.x[(size_t)b * K + k]) * h2f(lv);
@@ -141,8 +148,8 @@ __global__ __launch_bounds__(64) void k_gemv_generic(GemvArgs a) {
 // (the per-row form of lut_embed, compute-core/src/lut/evaluator.rs:176-197).
 // For 4-bit weights elements at k >= (K/8)*8 are written as 0, matching
 // lut_embed's shorter output zero-padded.
-// GI: 4-bit weights in the GI layout with G rows per group (lut and idx
-// both point at it).
+// GI: weights in the GI layout with G rows per group (lut and idx both
+// point at it).
 template <int BITS, bool GI = false>
 __global__ __launch_bounds__(256) void k_decode_rows(const uint8_t* lut, const uint8_t* idx, uint32_t N,
                                                      uint32_t K, uint32_t row0, uint32_t nrows, uint16_t* out,
@@ -158,12 +165,12 @@ __global__ __launch_bounds__(256) void k_decode_rows(const uint8_t* lut, const u
     if (r < N && k < keff) {
       uint32_t e;
       if (BITS == 4) {
-        const uint8_t byte = GI ? idx[gi_index_at(G, r, k, K)] : idx[(size_t)r * stride + (k >> 1)];
+        const uint8_t byte = GI ? idx[gi_index_at(G, r, k, K, 4)] : idx[(size_t)r * stride + (k >> 1)];
         e = (k & 1) ? (byte >> 4) : (byte & 15u);
       } else {
-        e = idx[(size_t)r * stride + k];
+        e = GI ? idx[gi_index_at(G, r, k, K, 8)] : idx[(size_t)r * stride + k];
       }
-      const uint8_t* l = lut + (GI ? gi_lut_offset(G, r, K) : (size_t)r * (2u << BITS)) + 2 * e;
+      const uint8_t* l = lut + (GI ? gi_lut_offset(G, r, K, BITS) : (size_t)r * (2u << BITS)) + 2 * e;
       v = (uint16_t)(l[0] | (l[1] << 8));
     }
     out[t] = v;

@@ -285,25 +285,206 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   }
 }
 
+// Chunk loads of k_gemv_lpr8 when the wave's chunk count is a compile-time
+// constant: first / ahead as for k_gemv_lpr.  cfg4 shape (14336 x 4096,
+// 8-bit, 56-row groups), MI355X, timing copies: (5, 5) with 2-chunk x
+// blocks 11.83 us, (4, 4) 11.85, (6, 6) 11.88, (8, 8) with 4-chunk blocks
+// 12.14; without the nontemporal hint on the index loads 13.57.
+constexpr int kLpr8First = 5;
+constexpr int kLpr8Ahead = 5;
+
+// 8-bit lane-per-row GEMV over GI weights (8-bit GI: [G x 512 B LUTs][K/16
+// chunks][G rows][16 B]; a chunk holds 16 elements).  The work layout of
+// k_gemv_lpr with S = 8 waves: lane l < G owns row G g + l, wave w a
+// contiguous 1/8 of the row's chunks, x in SGPRs.
+//  * Table: entry b of lane l's 256-entry LUT sits in the low half of LDS
+//    dword 64 b + l (bank-private, 64 KB per matrix); one v_perm builds the
+//    address from an index byte, one ds_read_b32 returns the fp16 value,
+//    and one v_perm packs two of them for v_dot2.  Per element one VALU op
+//    and one LDS read plus half a v_dot2 per batch vector.  Wave w builds
+//    entries 32 w .. 32 w + 31 of every lane's table from its 64-byte slice
+//    of the row's LUT.
+//  * NB = 1, 2, 4 or 8 vectors a pass (8 SGPRs per chunk and vector).
+//  * NCH > 0: the wave's chunk count as a compile-time constant, one
+//    straight-line sequence with kLpr8First / kLpr8Ahead; NCH = 0: a loop
+//    over blocks of 4 chunks with the next 4 in flight (chunk counts that are
+//    multiples of 4).
+// Requires K % 512 == 0, 16-byte aligned x and the weight block below 2 GiB.
+template <int S, int NM, int NB, int EPI, int NCH = 0>
+__global__ __launch_bounds__(64 * S) void k_gemv_lpr8(LprArgs a) {
+  static_assert(S == 8, "eight waves: 32 table entries each");
+  static_assert(NM == 1 || NM == 2, "one matrix or gate + up");
+  static_assert(NB == 1 || NB == 2 || NB == 4 || NB == 8, "batch vectors per pass");
+  static_assert(EPI == kLprPlain || (NM == 2 && NB == 1), "gate/up epilogues are single-vector");
+  constexpr int XB = NB >= 4 ? 1 : 2;  // x chunks per scalar block (8 SGPRs per chunk and vector)
+  constexpr int LB = 4;                // NCH = 0: chunks per loop trip (ring slots)
+  constexpr int R = NCH == 0 ? LB : (NCH < kLpr8First ? NCH : kLpr8First);
+  constexpr int DR = NCH == 0 ? LB : (R < kLpr8Ahead ? R : kLpr8Ahead);
+  constexpr int EPW = 256 / S;   // table entries each wave builds
+  constexpr int LL = EPW / 8;    // 16-byte LUT loads per lane and matrix
+  static_assert(NCH == 0 || NCH % XB == 0, "whole x blocks");
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+  __shared__ uint32_t lds[NM * kLprTableDw + S * NM * NB * 64];
+  float* red = reinterpret_cast<float*>(lds + NM * kLprTableDw);
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t g = blockIdx.x;
+  const uint32_t N = a.N, K = a.K, NC = K / 16;
+  const uint32_t G = a.G;
+  const uint32_t row = g * G + lane;
+  const bool live = lane < G;
+  const uint32_t nch = NC / S, c0 = w * nch;
+  const uint32_t gbytes = G * 512u + G * K;
+  const uint32_t gbase = g * gbytes;
+  const uint32_t nbytes = gridDim.x * gbytes;  // one workgroup per group
+  __amdgpu_buffer_rsrc_t ri[NM];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+    ri[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(m == 0 ? a.w : a.w2), (short)0, (int)nbytes, kBufferWord3);
+
+  // ---- this wave's 64-byte slice of the LUT of the lane's row (lanes past
+  // G read zeros through the range check; lanes past N the zero LUTs of the
+  // last group's padding rows)
+  u32x4v L[NM][LL];
+  const uint32_t lo = live ? gbase + lane * 512u + w * (EPW * 2u) : 0x80000000u;
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int i = 0; i < LL; i++) L[m][i] = __builtin_amdgcn_raw_buffer_load_b128(ri[m], lo + 16u * i, 0u, 0);
+
+  // ---- index chunks (unconditional loads; past the wave's range the offset
+  // is past the buffer's range and reads zeros without a memory access)
+  const uint32_t cstride = G * kGiChunk;
+  const uint32_t vbase = live ? gbase + G * 512u + (c0 * G + lane) * kGiChunk : 0x80000000u;
+  u32x4v ring[R][NM];
+  auto ldc = [&](uint32_t i, u32x4v (&dst)[NM]) {
+    const uint32_t vo = i < nch ? vbase + i * cstride : 0x80000000u;
+#pragma unroll
+    for (int m = 0; m < NM; m++) dst[m] = __builtin_amdgcn_raw_buffer_load_b128(ri[m], vo, 0u, kNontemporal);
+  };
+#pragma unroll
+  for (int u = 0; u < R; u++) ldc(u, ring[u]);
+
+  // x of vector b (vectors past nb read vector 0): one base pointer and
+  // scalar row offsets, so eight vectors' pointers do not hold 16 SGPRs
+  const u32x8* xw = reinterpret_cast<const u32x8*>(a.x) + c0;
+  const uint32_t xrow = K / 16;  // 32-byte x chunks per vector
+  u32x8 xs[NB][XB];
+  auto ldx = [&](uint32_t i) {
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int u = 0; u < XB; u++) xs[b][u] = xw[((uint32_t)b < a.nb ? (uint32_t)b : 0u) * xrow + i + u];
+  };
+  ldx(0);
+
+  // ---- bank-private tables: entry e at dword 64 e + lane, LUT[e] in the low half
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int i = 0; i < LL; i++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t d = L[m][i][q];
+        const uint32_t e = w * EPW + 8 * i + 2 * q;
+        lds[m * kLprTableDw + e * 64 + lane] = d & 0xFFFFu;
+        lds[m * kLprTableDw + (e + 1) * 64 + lane] = d >> 16;
+      }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+
+  const uint32_t lanebase = lane * 4u;
+  float acc[NM][NB][2];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) acc[m][b][0] = acc[m][b][1] = 0.0f;
+  auto chunk = [&](uint32_t c, int slot, int xu, bool refill) {
+    uint32_t v[NM][16];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const uint32_t ad = __builtin_amdgcn_perm(ring[slot][m][j >> 2], lanebase, 0x0C0C0000u | ((4u + (j & 3)) << 8));
+        v[m][j] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds + m * kLprTableDw) + ad);
+      }
+    if (refill) ldc(c + DR, ring[(slot + DR) % R]);
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int p = 0; p < 8; p++) {
+        const uint32_t pr = __builtin_amdgcn_perm(v[m][2 * p + 1], v[m][2 * p], 0x05040100u);
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[m][b][p & 1] = dot2(pr, xs[b][xu][p], acc[m][b][p & 1]);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (NCH > 0) {
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      if (c % XB == 0 && c != 0) ldx(c);
+      chunk(c, c % R, c % XB, c >= R - DR && c + DR < NCH);
+    }
+  } else {
+    for (uint32_t i = 0; i < nch; i += LB) {
+#pragma unroll
+      for (int u = 0; u < LB; u++) {
+        if (u % XB == 0 && (i != 0 || u != 0)) ldx(i + u);
+        chunk(i + u, u, u % XB, true);
+      }
+    }
+  }
+
+  // ---- wave partials -> LDS -> rows (waves 0 .. NB-1 finish one vector each)
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int b = 0; b < NB; b++) red[((w * NM + m) * NB + b) * 64 + lane] = acc[m][b][0] + acc[m][b][1];
+  __syncthreads();
+  if (w < (uint32_t)NB) {
+    const uint32_t b = w;
+    float s[NM];
+#pragma unroll
+    for (int m = 0; m < NM; m++) {
+      s[m] = 0.0f;
+#pragma unroll
+      for (int v = 0; v < S; v++) s[m] += red[((v * NM + m) * NB + b) * 64 + lane];
+    }
+    if (live && row < N && b < a.nb) {
+      if constexpr (EPI == kLprSwiglu)
+        a.y[row] = swiglu_h(s[0], s[1]);
+      else if constexpr (EPI == kLprPair) {
+        a.y[row] = f2h(s[0]);
+        a.y2[row] = f2h(s[1]);
+      } else
+        a.y[(size_t)b * N + row] = f2h(s[0]);
+    }
+  }
+}
+
 // Split-block payload (LUT block then index rows) -> GI with G rows per
-// group.  One thread per 16-byte piece of the GI block, in GI order: the
-// writes are contiguous, the reads 16 bytes each.  Rows past N get zero
-// LUTs and zero indices.
+// group, 4- or 8-bit.  One thread per 16-byte piece of the GI block, in GI
+// order: the writes are contiguous, the reads 16 bytes each.  Rows past N
+// get zero LUTs and zero indices.
 __global__ __launch_bounds__(256) void k_gi_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
-                                                 uint32_t N, uint32_t K, uint32_t G) {
-  const uint32_t NC = K / 32;
-  const uint32_t per_group = 2 * G + NC * G;  // 16-byte pieces per group
+                                                 uint32_t N, uint32_t K, uint32_t G, uint32_t bits) {
+  const uint32_t lp = gi_lut_bytes(bits) / 16;  // 16-byte pieces of one row's LUT
+  const uint32_t rb = K * bits / 8;             // index bytes per row
+  const uint32_t NC = rb / kGiChunk;
+  const uint32_t per_group = lp * G + NC * G;  // 16-byte pieces per group
   const size_t total = (size_t)((N + G - 1) / G) * per_group;
-  const uint8_t* sidx = src + (size_t)N * 32;
+  const uint8_t* sidx = src + (size_t)N * gi_lut_bytes(bits);
   for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (size_t)gridDim.x * blockDim.x) {
     const uint32_t g = (uint32_t)(t / per_group), p = (uint32_t)(t % per_group);
     uint4 v = make_uint4(0, 0, 0, 0);
-    if (p < 2 * G) {  // LUT piece: row p/2, half p%2
-      const uint32_t r = g * G + p / 2;
-      if (r < N) v = *reinterpret_cast<const uint4*>(src + (size_t)r * 32 + (p % 2) * 16);
+    if (p < lp * G) {  // LUT piece p % lp of row p / lp
+      const uint32_t r = g * G + p / lp;
+      if (r < N) v = *reinterpret_cast<const uint4*>(src + (size_t)r * gi_lut_bytes(bits) + (p % lp) * 16);
     } else {
-      const uint32_t q = p - 2 * G, c = q / G, r = g * G + q % G;
-      if (r < N) v = *reinterpret_cast<const uint4*>(sidx + (size_t)r * (K / 2) + (size_t)c * kGiChunk);
+      const uint32_t q = p - lp * G, c = q / G, r = g * G + q % G;
+      if (r < N) v = *reinterpret_cast<const uint4*>(sidx + (size_t)r * rb + (size_t)c * kGiChunk);
     }
     *reinterpret_cast<uint4*>(dst + t * 16) = v;
   }
@@ -320,10 +501,10 @@ __global__ __launch_bounds__(256) void k_gi_unpack(const uint8_t* __restrict__ s
     const uint32_t r = (uint32_t)(t / (2 + NC)), p = (uint32_t)(t % (2 + NC));
     if (p < 2)
       *reinterpret_cast<uint4*>(dst_lut + (size_t)r * 32 + p * 16) =
-          *reinterpret_cast<const uint4*>(src + gi_lut_offset(G, r, K) + p * 16);
+          *reinterpret_cast<const uint4*>(src + gi_lut_offset(G, r, K, 4) + p * 16);
     else
       *reinterpret_cast<uint4*>(dst_idx + (size_t)r * (K / 2) + (size_t)(p - 2) * kGiChunk) =
-          *reinterpret_cast<const uint4*>(src + gi_chunk_offset(G, r, p - 2, K));
+          *reinterpret_cast<const uint4*>(src + gi_chunk_offset(G, r, p - 2, K, 4));
   }
 }
 

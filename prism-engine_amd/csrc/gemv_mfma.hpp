@@ -33,9 +33,10 @@
 // bank, 64 KB for 32 8-bit rows with a 32x32 MFMA tile) removes them but
 // measured slower, its x operand padded to 32 rows and its table build
 // costing more than they save.
-// GI (4-bit only): the weights are in the GI layout with a.gi rows per
-// group (gemv_lpr.hpp; a.lut and a.idx both point at it): a lane's 16 index
-// bytes of a K group are one 16-byte chunk of its row.
+// GI: the weights are in the GI layout with a.gi rows per group
+// (gemv_lpr.hpp; a.lut and a.idx both point at it): a lane's index bytes of
+// a K group are one 16-byte chunk of its row (4-bit) or two consecutive
+// chunks, G * 16 bytes apart (8-bit).
 // Requires K % 128 == 0, 16-byte aligned x, nb <= 16 and the weight bytes
 // below 2 GiB.
 #pragma once
@@ -59,7 +60,6 @@ constexpr int kGmGroup = 128; // K elements per wave per loop trip (4 MFMA steps
 template <int BITS, bool GI = false>
 __global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
   static_assert(BITS == 4 || BITS == 8, "4- or 8-bit indices");
-  static_assert(!GI || BITS == 4, "GI is a 4-bit layout");
   constexpr int T = kGmTiles, RN = kGmRows, KW = kGmWaves, NT = 64 * kGmWaves;
   constexpr int IB = 32 * BITS / 8;  // index bytes per lane, row and group
   // 8-bit: [row][256] fp16; 4-bit: [tile][256][16] pair dwords
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(nb * K * 2u), kBufferWord3);
   const uint32_t G = GI ? a.gi : 0u;
-  const uint32_t wbytes = GI ? (uint32_t)gi_bytes(G, N, K) : N * (K * BITS / 8);
+  const uint32_t wbytes = GI ? (uint32_t)gi_bytes(G, N, K, BITS) : N * (K * BITS / 8);
   const __amdgpu_buffer_rsrc_t ri = __builtin_amdgcn_make_buffer_rsrc((void*)a.idx, (short)0, (int)wbytes, kBufferWord3);
   const uint32_t xv = n * K * 2u + kq * 64u;
   // per-lane VGPR offset of the lane's index bytes in group 0; the group's
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
   for (int t = 0; t < T; t++) {
     uint32_t r = n0 + 16 * t + n;
     r = r < N ? r : N - 1;
-    iv[t] = GI ? (uint32_t)gi_chunk_offset(G, r, kq, K) : r * (K * BITS / 8) + kq * IB;
+    iv[t] = GI ? (uint32_t)gi_chunk_offset(G, r, kq * (IB / 16), K, BITS) : r * (K * BITS / 8) + kq * IB;
   }
 
   struct Group {
@@ -104,8 +104,8 @@ __global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
     for (int t = 0; t < T; t++)
 #pragma unroll
       for (int j = 0; j < IB / 16; j++)
-        d.w[t][j] = __builtin_amdgcn_raw_buffer_load_b128(ri, iv[t] + 16 * j, GI ? k0 / 2u * G : k0 * BITS / 8,
-                                                          kNontemporal);
+        d.w[t][j] = __builtin_amdgcn_raw_buffer_load_b128(ri, iv[t] + (GI ? G * 16u : 16u) * j,
+                                                          GI ? k0 * BITS / 8u * G : k0 * BITS / 8, kNontemporal);
   };
   // B operand of tile t: the 8 elements whose index bits are `w`
   auto lookb = [&](int t, u32x2v_t w) {
@@ -162,12 +162,13 @@ __global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
   // barriers: __syncthreads would also wait for the group loads above.
   const uint32_t live = N - n0 < (uint32_t)RN ? N - n0 : (uint32_t)RN;
   if constexpr (BITS == 8) {
-    const uint4* src = reinterpret_cast<const uint4*>(a.lut + (size_t)n0 * 512);
     uint4* dst = reinterpret_cast<uint4*>(tbl);
 #pragma unroll
     for (int i = 0; i < RN * 32 / NT; i++) {
-      const uint32_t e = tid + NT * i;  // uint4 e of row e / 32
-      dst[e] = e < live * 32 ? src[e] : make_uint4(0, 0, 0, 0);
+      const uint32_t e = tid + NT * i;  // uint4 e % 32 of row n0 + e / 32 (GI: the rows may span two groups)
+      const uint4* src = reinterpret_cast<const uint4*>(
+          a.lut + (GI ? gi_lut_offset(G, n0 + e / 32, K, 8) : (size_t)(n0 + e / 32) * 512) + 16 * (e % 32));
+      dst[e] = e < live * 32 ? *src : make_uint4(0, 0, 0, 0);
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   } else {
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(64 * kGmWaves) void k_gemv_mfma(GemvArgs a) {
       // half tid % 2 of row n0 + tid / 2 (GI: the workgroup's rows may span two groups)
       const uint32_t r = n0 + tid / 2;
       const uint4* src =
-          reinterpret_cast<const uint4*>(a.lut + (GI ? gi_lut_offset(G, r, K) : (size_t)r * 32) + (tid % 2) * 16);
+          reinterpret_cast<const uint4*>(a.lut + (GI ? gi_lut_offset(G, r, K, 4) : (size_t)r * 32) + (tid % 2) * 16);
       reinterpret_cast<uint4*>(stage)[tid] = tid < live * 2 ? *src : make_uint4(0, 0, 0, 0);
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");

@@ -264,11 +264,16 @@ hipStream_t pick_stream(prism_hip_ctx* ctx, void* stream) {
 // 2 x 14336 x 4096 12.3 us; 4864 x 896 3.5 against 3.05 us and 896 x 4864
 // 6.3 against 3.2 us (too few rows), 2 x 18944 x 3584 19.6 against 17.6 us
 // (more than 64 rows per CU: two rounds), so those stay split-block.
+// 8-bit matrices take the same groups when K % 512 == 0 (k_gemv_lpr8's
+// eight waves split a row into whole blocks of four 16-byte chunks):
+// 14336 x 4096 at 1 / 2 / 4 / 8 vectors 11.8 / 12.1 / 13.6 / 18.2 us
+// against 14.3 / 15.5 / 18.2 / 19.8 on split-block weights.
 uint32_t gi_rows(const prism_hip_ctx* ctx, uint32_t dm, uint32_t dn, uint32_t bits) {
-  if (bits != 4 || dn % 64 != 0 || dn < 2048) return 0;
+  if (dn < 2048 || (bits == 4 && dn % 64 != 0) || (bits == 8 && dn % 512 != 0) || (bits != 4 && bits != 8))
+    return 0;
   const uint32_t ncu = (uint32_t)ctx->num_cu;
   const uint32_t G = ((dm + ncu - 1) / ncu + 7) / 8 * 8;
-  if (G < 32 || G > (uint32_t)prism::kGiMaxRows || prism::gi_bytes(G, dm, dn) >= (1ull << 31)) return 0;
+  if (G < 32 || G > (uint32_t)prism::kGiMaxRows || prism::gi_bytes(G, dm, dn, bits) >= (1ull << 31)) return 0;
   return G;
 }
 
@@ -516,8 +521,115 @@ void launch_lpr(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
     hipLaunchKernelGGL((prism::k_gemv_lpr<S, NM, NB, EPI>), groups, dim3(64 * S), 0, st, a);
 }
 
+// 8-bit GI weights: k_gemv_lpr8 with the wave's chunk count as a
+// compile-time constant when it is 16, 32 or 64 (K = 2048 / 4096 / 8192),
+// else the loop over 4-chunk blocks.  Eight vectors a pass only with a
+// compile-time count (the loop form runs out of SGPRs for their x).
+bool lpr8_static(uint32_t K) {
+  const uint32_t nch = K / 16 / 8;
+  return nch == 16 || nch == 32 || nch == 64;
+}
+template <int NM, int NB, int EPI>
+void launch_lpr8(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
+  const uint32_t nch = a.K / 16 / 8;
+  if (nch == 32)
+    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI, 32>), groups, dim3(512), 0, st, a);
+  else if (nch == 16)
+    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI, 16>), groups, dim3(512), 0, st, a);
+  else if (nch == 64)
+    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI, 64>), groups, dim3(512), 0, st, a);
+  else if constexpr (NB < 8)
+    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI>), groups, dim3(512), 0, st, a);
+}
+
+// GEMV over 8-bit GI weights: gate + up (SwiGLU, or the pair with d_y2) in
+// one k_gemv_lpr8 pass; one matrix in passes of 1 / 2 / 4 / 8 vectors
+// (k_gemv_lpr8), or of up to 16 on the matrix cores from 9 vectors on (from
+// 5 when the chunk count is not a compile-time one) (k_gemv_mfma<8, GI>).
+// x not 16-byte aligned: the generic kernel.
+int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
+                    uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
+  const uint32_t N = w->dim_m, K = w->dim_n;
+  const bool aligned = reinterpret_cast<uintptr_t>(d_x) % 16 == 0;
+  const uint32_t G = w->gi;
+  const dim3 groups((N + G - 1) / G);
+  prism::GemvArgs ga{};
+  ga.gi = G;
+  ga.lut = ga.idx = w->d;
+  ga.N = N;
+  ga.K = K;
+  if (w2) {
+    ga.lut2 = ga.idx2 = w2->d;
+    ga.x = reinterpret_cast<const uint16_t*>(d_x);
+    ga.y = reinterpret_cast<uint16_t*>(d_y);
+    ga.y2 = reinterpret_cast<uint16_t*>(d_y2);
+    ga.nb = 1;
+    if (aligned) {
+      prism::LprArgs a{};
+      a.G = G;
+      a.w = w->d;
+      a.w2 = w2->d;
+      a.x = ga.x;
+      a.y = ga.y;
+      a.y2 = ga.y2;
+      a.N = N;
+      a.K = K;
+      a.nb = 1;
+      if (d_y2)
+        launch_lpr8<2, 1, prism::kLprPair>(groups, st, a);
+      else
+        launch_lpr8<2, 1, prism::kLprSwiglu>(groups, st, a);
+    } else if (d_y2) {
+      hipLaunchKernelGGL((prism::k_gemv_generic<8, prism::kGenPair, true>), dim3(N), dim3(64), 0, st, ga);
+    } else {
+      hipLaunchKernelGGL((prism::k_gemv_generic<8, prism::kGenSwiglu, true>), dim3(N), dim3(64), 0, st, ga);
+    }
+    HIP_TRY(ctx, hipGetLastError());
+    return PRISM_HIP_OK;
+  }
+  for (uint32_t b0 = 0; b0 < nb;) {
+    const uint16_t* x = reinterpret_cast<const uint16_t*>(d_x) + (size_t)b0 * K;
+    uint16_t* y = reinterpret_cast<uint16_t*>(d_y) + (size_t)b0 * N;
+    const uint32_t left = nb - b0;
+    uint32_t chunk;
+    if (!aligned) {
+      ga.x = x;
+      ga.y = y;
+      ga.nb = chunk = left;
+      hipLaunchKernelGGL((prism::k_gemv_generic<8, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, ga);
+    } else if (left >= 9 || (left >= 5 && !lpr8_static(K))) {
+      ga.x = x;
+      ga.y = y;
+      ga.nb = chunk = left < (uint32_t)prism::kGmMaxNb ? left : (uint32_t)prism::kGmMaxNb;
+      hipLaunchKernelGGL((prism::k_gemv_mfma<8, true>), dim3((N + prism::kGmRows - 1) / prism::kGmRows),
+                         dim3(64 * prism::kGmWaves), 0, st, ga);
+    } else {
+      prism::LprArgs a{};
+      a.G = G;
+      a.w = w->d;
+      a.x = x;
+      a.y = y;
+      a.N = N;
+      a.K = K;
+      a.nb = chunk = left;
+      if (left == 1)
+        launch_lpr8<1, 1, prism::kLprPlain>(groups, st, a);
+      else if (left == 2)
+        launch_lpr8<1, 2, prism::kLprPlain>(groups, st, a);
+      else if (left <= 4)
+        launch_lpr8<1, 4, prism::kLprPlain>(groups, st, a);
+      else
+        launch_lpr8<1, 8, prism::kLprPlain>(groups, st, a);
+    }
+    HIP_TRY(ctx, hipGetLastError());
+    b0 += chunk;
+  }
+  return PRISM_HIP_OK;
+}
+
 int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
                    uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
+  if (w->bits == 8) return launch_gemv_gi8(ctx, w, w2, d_x, nb, d_y, d_y2, st);
   const uint32_t N = w->dim_m, K = w->dim_n;
   const bool aligned = reinterpret_cast<uintptr_t>(d_x) % 16 == 0;
   const uint32_t G = w->gi;
@@ -733,15 +845,19 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
       sk8 = sk8 < 4 ? sk8 : 4;
       sk8 = sk8 < nsteps / 8 ? sk8 : nsteps / 8;
     }
-    if (M > 256 || sk8 >= 2) {
+    // GI weights always take k_gemm8 (unsplit when K cannot split)
+    if (M > 256 || sk8 >= 2 || w->gi) {
       const uint32_t tiles8 = ((M + prism::GM8_BM - 1) / prism::GM8_BM) * nt8;
-      const uint32_t nsplit8 = M <= 256 ? sk8 : 1;
-      const void* fn = nsplit8 > 1 ? reinterpret_cast<const void*>(&prism::k_gemm8<true>)
-                                   : reinterpret_cast<const void*>(&prism::k_gemm8<false>);
+      const uint32_t nsplit8 = M <= 256 && sk8 >= 2 ? sk8 : 1;
+      const void* fn = w->gi ? (nsplit8 > 1 ? reinterpret_cast<const void*>(&prism::k_gemm8<true, true>)
+                                            : reinterpret_cast<const void*>(&prism::k_gemm8<false, true>))
+                             : (nsplit8 > 1 ? reinterpret_cast<const void*>(&prism::k_gemm8<true>)
+                                            : reinterpret_cast<const void*>(&prism::k_gemm8<false>));
       return launch_gemm_blocks(ctx, fn, tiles8, nsteps, nsplit8, w, d_X, M, d_Y, st, fixed);
     }
   }
-  // GI weights (K % 64 == 0, below 2 GiB) always take k_gemm_w4 above.
+  // GI weights (4-bit: K % 64 == 0, below 2 GiB; 8-bit: K % 512 == 0) always
+  // take k_gemm_w4 or k_gemm8 above.
   if (w->gi) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no GEMM kernel for this GI weight (%ux%u)", N, K);
   const uint32_t tiles = ((M + prism::GEMM_BM - 1) / prism::GEMM_BM) * ((N + prism::GEMM_BN - 1) / prism::GEMM_BN);
   const uint8_t* lut = w->lut();
@@ -767,7 +883,8 @@ int launch_decode(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, 
   uint16_t* out = reinterpret_cast<uint16_t*>(d_out);
   uint32_t G = w->gi;
   void* args[] = {&lut, &idx, &N, &K, &row0, &nrows, &out, &G};
-  const void* fn = w->bits == 8 ? reinterpret_cast<const void*>(&prism::k_decode_rows<8>)
+  const void* fn = w->bits == 8 ? (w->gi ? reinterpret_cast<const void*>(&prism::k_decode_rows<8, true>)
+                                        : reinterpret_cast<const void*>(&prism::k_decode_rows<8>))
                    : w->gi      ? reinterpret_cast<const void*>(&prism::k_decode_rows<4, true>)
                                 : reinterpret_cast<const void*>(&prism::k_decode_rows<4>);
   HIP_TRY(ctx, hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(256), args, 0, st));
@@ -907,7 +1024,7 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
     delete w;
     return nullptr;
   };
-  hipError_t e = hipMalloc(&w->d, w->gi ? prism::gi_bytes(w->gi, dm, dn) : bytes);
+  hipError_t e = hipMalloc(&w->d, w->gi ? prism::gi_bytes(w->gi, dm, dn, bits) : bytes);
   if (e != hipSuccess) {
     w->d = nullptr;
     fail(ctx, PRISM_HIP_ERR_DEVICE, "weight upload (%zu bytes): hipMalloc: %s", bytes, hipGetErrorString(e));
@@ -929,10 +1046,10 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
       s = ctx->d_upload;
     }
     if (rc == PRISM_HIP_OK) {
-      const size_t pieces = prism::gi_bytes(w->gi, dm, dn) / 16;
+      const size_t pieces = prism::gi_bytes(w->gi, dm, dn, bits) / 16;
       const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
       hipLaunchKernelGGL(prism::k_gi_pack, dim3(grid), dim3(256), 0, ctx->stream,
-                         reinterpret_cast<const uint8_t*>(s), w->d, dm, dn, w->gi);
+                         reinterpret_cast<const uint8_t*>(s), w->d, dm, dn, w->gi, bits);
       e = hipGetLastError();
       if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "GI pack: %s", hipGetErrorString(e));
     }

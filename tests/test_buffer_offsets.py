@@ -51,24 +51,24 @@ GM_WAVES = _const("gemv_mfma.hpp", "kGmWaves")
 GM_GROUP = _const("gemv_mfma.hpp", "kGmGroup")
 
 
-def gi_rows(N, K, num_cu=256):
+def gi_rows(N, K, num_cu=256, bits=4):
     """The library's layout rule (prism_hip.hip gi_rows)."""
-    if K % 64 or K < 2048:
+    if K < 2048 or K % (64 if bits == 4 else 512):
         return 0
     G = (-(-N // num_cu) + 7) // 8 * 8
     return G if 32 <= G <= GI_MAX else 0
 
 
-def gi_group_bytes(G, K):
-    return G * 32 + G * (K // 2)
+def gi_group_bytes(G, K, bits=4):
+    return G * (2 << bits) + G * (K * bits // 8)
 
 
-def gi_bytes(G, N, K):
-    return -(-N // G) * gi_group_bytes(G, K)
+def gi_bytes(G, N, K, bits=4):
+    return -(-N // G) * gi_group_bytes(G, K, bits)
 
 
-def gi_chunk_offset(G, r, c, K):
-    return (r // G) * gi_group_bytes(G, K) + G * 32 + (c * G + r % G) * GI_CHUNK
+def gi_chunk_offset(G, r, c, K, bits=4):
+    return (r // G) * gi_group_bytes(G, K, bits) + G * (2 << bits) + (c * G + r % G) * GI_CHUNK
 
 
 def _check(voff, soff, width, num_records, alloc, what):
@@ -155,6 +155,7 @@ def test_gemm_w4_offsets(M, N, K, MI, GI):
 @pytest.mark.parametrize("N,K,nb,bits,GI", [
     (14336, 4096, 8, 4, True), (14336, 4096, 16, 4, False), (14336, 4096, 5, 8, False),
     (4099, 1024, 3, 4, False), (9100, 2048, 16, 4, True), (1000, 384, 4, 8, False),
+    (14336, 4096, 16, 8, True), (9100, 2048, 9, 8, True), (8192, 2560, 5, 8, True),
 ])
 def test_gemv_mfma_offsets(N, K, nb, bits, GI):
     lane = np.arange(64)
@@ -162,8 +163,9 @@ def test_gemv_mfma_offsets(N, K, nb, bits, GI):
     IB = 32 * bits // 8
     ng = K // GM_GROUP
     x_alloc = nb * K * 2
-    G = gi_rows(N, K) if GI else 0
-    wbytes = gi_bytes(G, N, K) if GI else N * (K * bits // 8)
+    G = gi_rows(N, K, bits=bits) if GI else 0
+    assert not GI or G
+    wbytes = gi_bytes(G, N, K, bits) if GI else N * (K * bits // 8)
     row_b = K * bits // 8
     for blk in range(-(-N // GM_ROWS)):
         n0 = blk * GM_ROWS
@@ -179,16 +181,22 @@ def test_gemv_mfma_offsets(N, K, nb, bits, GI):
                 for t in range(GM_TILES):
                     r = np.minimum(n0 + 16 * t + n, N - 1)
                     if GI:
-                        iv = gi_chunk_offset(G, r, kq, K)
-                        soff = k0 // 2 * G
-                        end = (r // G + 1) * gi_group_bytes(G, K)
+                        # gemv_mfma.hpp:92,107-108: chunk kq * IB / 16 (+ j), G * 16 bytes apart
+                        iv = gi_chunk_offset(G, r, kq * (IB // 16), K, bits)
+                        soff = k0 * bits // 8 * G
+                        step = G * 16
+                        end = (r // G + 1) * gi_group_bytes(G, K, bits)
                     else:
                         iv = r * row_b + kq * IB
                         soff = k0 * bits // 8
+                        step = 16
                         end = (r + 1) * row_b
                     for j in range(IB // 16):
-                        perf = _check(iv + 16 * j, soff, 16, wbytes, wbytes, "gemv_mfma index")
-                        assert ((iv + 16 * j + soff + 16) <= end)[perf].all(), "index load leaves its row/group"
+                        perf = _check(iv + step * j, soff, 16, wbytes, wbytes, "gemv_mfma index")
+                        assert ((iv + step * j + soff + 16) <= end)[perf].all(), "index load leaves its row/group"
+                        if GI:  # the chunk is the lane's own row's chunk k0 / 16 + 2 kq + j of the row
+                            c = (iv + step * j + soff - (r // G) * gi_group_bytes(G, K, bits) - G * (2 << bits)) // 16
+                            assert (c % G == r % G).all() and (c // G == k0 * bits // 128 + kq * (IB // 16) + j).all()
 
 
 # ---- k_gemv_tile (gemv_tile.hpp:229-262) and k_gemv_lpr (gemv_lpr.hpp:120-135):
@@ -234,3 +242,33 @@ def test_gemv_lpr_offsets(N, K):
                     perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr chunk")
                     assert (perf == ((lane < G) & (i < nch))).all()
                     assert ((vo + 16) <= base + gi_group_bytes(G, K))[perf].all()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (16384, 2048), (8192, 2560)])
+def test_gemv_lpr8_offsets(N, K):
+    """k_gemv_lpr8 (gemv_lpr.hpp): each wave's 64-byte slice of the lane's
+    LUT, then chunk c of its range or an offset past the range; lanes past G
+    always past the range; nothing in the scalar offset."""
+    G = gi_rows(N, K, bits=8)
+    assert G
+    S, NC = 8, K // 16
+    nch = NC // S
+    lane = np.arange(64)
+    ngroups = -(-N // G)
+    nbytes = ngroups * gi_group_bytes(G, K, 8)  # gridDim.x * gbytes
+    assert nbytes == gi_bytes(G, N, K, 8)
+    for w in range(S):
+        c0 = w * nch
+        for g in (0, ngroups - 1):
+            base = g * gi_group_bytes(G, K, 8)
+            lo = np.where(lane < G, base + lane * 512 + w * 64, 0x80000000)
+            for i in range(4):
+                perf = _check(lo + 16 * i, 0, 16, nbytes, nbytes, "gemv_lpr8 LUT")
+                assert (perf == (lane < G)).all()
+                assert ((lo + 16 * i + 16) <= base + (lane + 1) * 512)[perf].all(), "LUT load leaves its row"
+            vbase = np.where(lane < G, base + G * 512 + (c0 * G + lane) * GI_CHUNK, 0x80000000)
+            for i in range(nch + 8):  # the ring issues loads past the range
+                vo = vbase + i * G * GI_CHUNK if i < nch else np.full(64, 0x80000000)
+                perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr8 chunk")
+                assert (perf == ((lane < G) & (i < nch))).all()
+                assert ((vo + 16) <= base + gi_group_bytes(G, K, 8))[perf].all()

@@ -1,15 +1,18 @@
-"""The GI device layout (4-bit weights with rows of >= 2048 elements,
-K % 64 == 0, in groups of G = 32..64 rows, G = ceil(N / num_cu) rounded up
-to a multiple of 8) and the two-output gate/up GEMV, through the C ABI
-against the CPU oracle.
+"""The GI device layout (weights with rows of >= 2048 elements, K % 64 == 0
+at 4 bits and K % 512 == 0 at 8, in groups of G = 32..64 rows,
+G = ceil(N / num_cu) rounded up to a multiple of 8) and the two-output
+gate/up GEMV, through the C ABI against the CPU oracle.
 
 Every operation on a weight must give the same results whatever device
-layout the library chose for it: the lane-per-row GEMV (1..2 vectors), the
-matrix-core GEMV over GI (3+ vectors), the generic kernel (unaligned x),
-the GEMM, the row decode and the decode-step model's copies.  Shapes (on a
-256-CU MI355X): 14336 x 4096 (56-row groups, 256 of them), 9100 x 2048
-(40-row groups, 228 with a ragged last one), 8192 x 2112 (32-row groups;
-K % 128 != 0: no matrix-core pass), 16384 x 2048 (64-row groups).
+layout the library chose for it: the lane-per-row GEMVs (4-bit: 1..2
+vectors; 8-bit: 1..8), the matrix-core GEMV over GI (more vectors), the
+generic kernel (unaligned x), the GEMM, the row decode and the decode-step
+model's copies.  4-bit shapes (on a 256-CU MI355X): 14336 x 4096 (56-row
+groups, 256 of them), 9100 x 2048 (40-row groups, 228 with a ragged last
+one), 8192 x 2112 (32-row groups; K % 128 != 0: no matrix-core pass),
+16384 x 2048 (64-row groups).  8-bit shapes: 14336 x 4096 and 9100 x 2048
+(chunk counts the 8-bit kernel takes as compile-time constants), 8192 x
+2560 (its loop form), 16384 x 2048.
 """
 import numpy as np
 import pytest
@@ -37,7 +40,7 @@ def _check(y, ref, what):
 
 def _gi(N, K, bits=4, num_cu=256):
     """The library's layout rule (prism_hip.hip gi_rows): the group rows, or 0."""
-    if bits != 4 or K % 64 or K < 2048:
+    if K < 2048 or bits not in (4, 8) or K % (64 if bits == 4 else 512):
         return 0
     G = (-(-N // num_cu) + 7) // 8 * 8
     return G if 32 <= G <= 64 else 0
@@ -274,3 +277,124 @@ def test_gi_model_step(pe, oracle, gpu_ctx):
     err = _rel(got, want)
     assert err <= TOL, f"logits rel err {err:.3e}"
     m.close()
+
+
+GI8_SHAPES = [(14336, 4096), (9100, 2048), (8192, 2560), (16384, 2048)]
+
+
+@pytest.mark.parametrize("N,K", GI8_SHAPES)
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 20])
+def test_gi8_gemv(pe, oracle, gpu_ctx, N, K, batch):
+    """8-bit GI: k_gemv_lpr8 passes of 1 / 2 / 4 / 8 vectors and the
+    matrix-core GEMV over GI from 9 vectors on (from 5 with the loop form)."""
+    assert _gi(N, K, 8)
+    if N * K > 4 * 10**7 and batch in (3, 5, 9):
+        pytest.skip("odd batches covered at the smaller shapes")
+    t = pe.synth_tensor(N, K, 8, seed=N + K + batch + 8)
+    x = pe.synth_x(batch, K, seed=batch * 5 + 2)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi8 gemv {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    ref = oracle.gemv(x, t.payload, N, K, 8, threads=8)
+    _check(y, ref, f"GI8 {N}x{K} batch {batch}")
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (8192, 2560)])
+def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
+    """One-hot x: every output is LUT_r[idx(r, k)] exactly, through the
+    8-bit lane-per-row GEMV at 1 and 4 vectors and the matrix-core GEMV over
+    GI (eleven vectors)."""
+    t = pe.synth_tensor(N, K, 8, seed=K + 13)
+    lut, idx = pe.unpack_payload(t.payload, N, K, 8)
+    ks = [0, 1, 15, 16, 17, K // 2 + 5, K // 3, K - 17, K - 16, K - 2, K - 1]
+    x = np.zeros((len(ks), K), dtype=np.float16)
+    for i, k in enumerate(ks):
+        x[i, k] = 1.0
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi8 one-hot {N}x{K}", flush=True)
+    ys = gpu_ctx.gemv(w, x.view(np.uint16))
+    y4 = gpu_ctx.gemv(w, x[:4].view(np.uint16))
+    for i, k in enumerate(ks):
+        want = lut[np.arange(N), idx[:, k]]
+        want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
+        y1 = gpu_ctx.gemv(w, x[i:i + 1].view(np.uint16))[0]
+        assert np.array_equal(y1, want), f"column {k}, one vector"
+        assert np.array_equal(ys[i], want), f"column {k}, eleven vectors"
+        if i < 4:
+            assert np.array_equal(y4[i], want), f"column {k}, four vectors"
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+def test_gi8_unaligned_x_and_decode_rows(pe, oracle, gpu_ctx, N, K):
+    """8-bit GI: x not 16-byte aligned takes the generic kernel; row decode
+    and lut_embed are the oracle's bytes exactly (ragged last group too)."""
+    import torch
+    t = pe.synth_tensor(N, K, 8, seed=N - K + 8)
+    x = pe.synth_x(2, K, seed=6)
+    w = gpu_ctx.upload_tensor(t)
+    buf = torch.zeros(2 * K + 8, dtype=torch.int16, device="cuda")
+    buf[1:1 + 2 * K] = torch.from_numpy(x.reshape(-1).view(np.int16)).cuda()
+    dy = torch.empty(2 * N, dtype=torch.int16, device="cuda")
+    print(f"gi8 unaligned {N}x{K}", flush=True)
+    gpu_ctx.gemv_dev(w, buf[1:], 2, dy)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy().view(np.uint16).reshape(2, N)
+    _check(y, oracle.gemv(x, t.payload, N, K, 8, threads=8), f"GI8 {N}x{K} unaligned x")
+    for r0, nr in [(0, 3), (63, 2), (N - 5, 5), (N // 2, 64)]:
+        out = torch.empty(nr * K, dtype=torch.int16, device="cuda")
+        gpu_ctx.decode_rows_dev(w, r0, nr, out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(np.uint16).reshape(nr, K)
+        want = oracle.decode_rows(t.payload, N, K, 8, r0, nr)
+        assert np.array_equal(got, want), f"rows {r0}..{r0 + nr}"
+    for tok in (0, 64, N - 1):
+        assert np.array_equal(gpu_ctx.lut_embed(w, tok), oracle.decode_rows(t.payload, N, K, 8, tok, 1)[0])
+    w.free()
+
+
+@pytest.mark.parametrize("N,K", [(14336, 4096), (8192, 2560)])
+def test_gi8_gateup_swiglu_and_upload_dev(pe, oracle, gpu_ctx, N, K):
+    """8-bit GI gate/up with the SwiGLU epilogue against the oracle; a
+    device-side payload regrouped like a host one."""
+    import torch
+    tg = pe.synth_tensor(N, K, 8, seed=N + 15)
+    tu = pe.synth_tensor(N, K, 8, seed=N + 16)
+    x = pe.synth_x(1, K, seed=N + 17)
+    wg, wu = gpu_ctx.upload_tensor(tg), gpu_ctx.upload_tensor(tu)
+    print(f"gi8 gate_up {N}x{K}", flush=True)
+    y = gpu_ctx.gateup_swiglu(wg, wu, x)
+    ref = oracle.gateup_swiglu(x[0], tg.payload, tu.payload, N, K, 8, threads=8)
+    _check(y, ref, f"GI8 gate_up + SwiGLU {N}x{K}")
+    dpay = torch.from_numpy(tg.payload.view(np.int8)).cuda()
+    w_dev = gpu_ctx.upload_dev(dpay, N, K, 8)
+    assert np.array_equal(gpu_ctx.gemv(wg, x), gpu_ctx.gemv(w_dev, x))
+    for w in (wg, wu, w_dev):
+        w.free()
+
+
+@pytest.mark.parametrize("M", [24, 64, 200, 300])
+def test_gi8_gemm(pe, oracle, gpu_ctx, M):
+    """8-bit prefill GEMM over GI weights with a ragged last group (40-row
+    groups, so a 128-row block spans four of them): GEMV passes (24 rows),
+    split K (64, 200; 2048 / 64 = 32 K steps) and whole-K blocks (300);
+    every row against the float32 product of the decoded weights, a spread
+    of rows against the oracle."""
+    N, K = 9100, 2048
+    t = pe.synth_tensor(N, K, 8, seed=M + 80)
+    X = pe.synth_x(M, K, seed=M + 81)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi8 gemm M={M}", flush=True)
+    Y = gpu_ctx.gemm(w, X)
+    dense = oracle.decode_rows(t.payload, N, K, 8, 0, N).view(np.float16).astype(np.float32)
+    Yf = X.view(np.float16).astype(np.float32) @ dense.T
+    got = Y.view(np.float16).astype(np.float32)
+    for m in range(M):
+        err = np.max(np.abs(got[m] - Yf[m])) / np.max(np.abs(Yf[m]))
+        assert err <= TOL, f"row {m}: {err:.3e}"
+    rows = sorted(set([0, M // 3, M // 2, M - 1]))
+    ref = oracle.gemm(np.ascontiguousarray(X[rows]), t.payload, N, K, 8, threads=8)
+    for i, m in enumerate(rows):
+        assert _rel(Y[m], ref[i]) <= TOL
+    w.free()
