@@ -21,8 +21,8 @@ work), palettize (the palette compiler: one step palettizes every matrix of
 a Qwen2.5-0.5B-architecture model, fp32 N(0, 0.02) weights resident in HBM,
 k=16, max_iter=50 as compile_to_cimage uses: fp32 params/s), floor (the
 read floor the GEMVs are held to: one launch of the library's streaming-read
-kernel over as many bytes as the hero GEMV reads, rotated the same way),
-load (a step is one load_cimage of a Qwen2.5-0.5B-sized 4-bit .cimage: mmap,
+kernel over as many bytes as the hero GEMV reads, rotated the same way;
+floor8 the same over config 4's 66 MB), load (a step is one load_cimage of a Qwen2.5-0.5B-sized 4-bit .cimage: mmap,
 every tensor through the pinned staging ring, one wait; GB/s of payload).
 """
 from __future__ import annotations
@@ -60,6 +60,8 @@ WORKLOADS = {
     "palettize": ("palettize", 4, 0, 0, 1),
     # the read floor: one streaming-read launch over the hero's weight bytes
     "floor": ("floor", 4, 14336, 4096, 1),
+    # the same over config 4's bytes (8-bit 14336 x 4096: 66 MB)
+    "floor8": ("floor", 8, 14336, 4096, 1),
     # .cimage -> device: load_cimage of a Qwen2.5-0.5B-sized file
     "load": ("load", 4, 0, 0, 1),
 }
@@ -623,7 +625,7 @@ def main() -> int:
         unit = "GB/s"
         metric = ("palettized GEMV effective HBM GB/s (% of 8 TB/s peak), 4-bit, batch 1"
                   if args.workload == "hero" and batch == 1 else
-                  "streaming-read floor GB/s (one launch over the hero's weight bytes)"
+                  f"streaming-read floor GB/s (one launch over the {'hero' if bits == 4 else 'config-4'} weight bytes)"
                   if kind == "floor" else
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
