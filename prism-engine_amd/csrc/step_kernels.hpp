@@ -147,15 +147,37 @@ constexpr int kAttnPassPos = 256;  // positions per pass: 16 per wave
 constexpr int kAttnPasses = 8;
 constexpr int kAttnMaxSeq = kAttnSplits * kAttnPassPos * kAttnPasses;
 
+// One DPP step: v's value from the lane that `ctrl` selects; rows outside
+// `rows` (and lanes with no source) give `fill`.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float v, float fill) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill), __builtin_bit_cast(int, v),
+                                                               CTRL, ROWS, 0xF, false));
+}
+// Wave-wide max and sum, the result in every lane: DPP within each row of
+// 16 lanes (quad_perm xor 1, xor 2, half-row mirror, row mirror), the row
+// broadcasts 15 and 31 into lane 63, and a read of lane 63.  All of it stays
+// in the VALU, where a ds_bpermute butterfly costs an LDS round trip per
+// step; these reductions sit on the attention's critical path (MI355X,
+// config-3 attention graph-launched alone: 5.59 -> 5.19 us per launch).
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  const float ninf = -INFINITY;
+  v = fmaxf(v, dpp_f<0xB1, 0xF>(v, ninf));
+  v = fmaxf(v, dpp_f<0x4E, 0xF>(v, ninf));
+  v = fmaxf(v, dpp_f<0x141, 0xF>(v, ninf));
+  v = fmaxf(v, dpp_f<0x140, 0xF>(v, ninf));
+  v = fmaxf(v, dpp_f<0x142, 0xA>(v, ninf));
+  v = fmaxf(v, dpp_f<0x143, 0xC>(v, ninf));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += dpp_f<0xB1, 0xF>(v, 0.0f);
+  v += dpp_f<0x4E, 0xF>(v, 0.0f);
+  v += dpp_f<0x141, 0xF>(v, 0.0f);
+  v += dpp_f<0x140, 0xF>(v, 0.0f);
+  v += dpp_f<0x142, 0xA>(v, 0.0f);
+  v += dpp_f<0x143, 0xC>(v, 0.0f);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
@@ -290,8 +312,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_step_attention(AttnArgs a) {
       for (int d = 0; d < 16; d++) part += s_q[16 * qd + d] * s_knew[16 * qd + d];
     }
     // quarters (0+1) + (2+3): the same value in all 4 lanes of a position
-    part += __shfl_xor(part, 1, 64);
-    part += __shfl_xor(part, 2, 64);
+    part += dpp_f<0xB1, 0xF>(part, 0.0f);
+    part += dpp_f<0x4E, 0xF>(part, 0.0f);
     const float sc = (p < p1) ? part / den : -INFINITY;
     const float m_new = fmaxf(m_run, wave_max(sc));  // finite: the slice holds a position
     const float corr = expf(m_run - m_new);          // 0 on the first slice
