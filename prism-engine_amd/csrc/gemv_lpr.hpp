@@ -1,5 +1,6 @@
-// gemv_lpr.hpp -- lane-per-row palettized GEMV for gfx950 over the
-// group-interleaved 4-bit device layout (GI), and the layout itself.
+// gemv_lpr.hpp -- lane-per-row palettized GEMVs for gfx950 over the
+// group-interleaved device layout (GI), 4-bit (k_gemv_lpr) and 8-bit
+// (k_gemv_lpr8, further down), and the layout itself.
 //
 // y[b, r] = f16( sum_k f32(x[b, k]) * f32(LUT_r[idx(r, k)]) ): the
 // arithmetic of lut_gemv_cpu (compute-core/src/lut/evaluator.rs:21-44),
@@ -8,12 +9,14 @@
 // the CPU path (evaluator.rs:78-83,209-225, engine_impl.rs:1349-1374) or the
 // two raw outputs of fused_gate_up.metal (templates/fused_gate_up.metal:16-97).
 //
-// GI device layout (written at upload by k_gi_pack, 4-bit, K % 64 == 0),
-// G <= 64 rows per group, chosen at upload so that the groups fill the GPU:
-//   ceil(N/G) row groups of gi_group_bytes(G, K) bytes each:
-//     [G x 32 B fp16 LUTs of the group's rows][K/32 chunks][G rows][16 B]
+// GI device layout (written at upload by k_gi_pack; 4-bit with K % 64 == 0,
+// 8-bit with K % 512 == 0), G <= 64 rows per group, chosen at upload so that
+// the groups fill the GPU:
+//   ceil(N/G) row groups of gi_group_bytes(G, K, bits) bytes each:
+//     [G row LUTs (32 B fp16 at 4 bits, 512 B at 8)][row bytes / 16 chunks][G rows][16 B]
 //   chunk c of row r holds index bytes 16c .. 16c+15 of the split-block row
-//   (elements 32c .. 32c+31, element 2i = low nibble of byte i).  Rows past
+//   (4-bit: elements 32c .. 32c+31, element 2i = low nibble of byte i;
+//   8-bit: elements 16c .. 16c+15).  Rows past
 //   N in the last group are zero.  A wave's 16-byte-per-lane load reads
 //   chunk c of the group's G rows: 16 G bytes contiguous.  A group's LUTs
 //   sit right before its chunks, so they come from the same DRAM pages as
@@ -299,8 +302,8 @@ constexpr int kLpr8Ahead = 5;
 //  * Table: entry b of lane l's 256-entry LUT sits in the low half of LDS
 //    dword 64 b + l (bank-private, 64 KB per matrix); one v_perm builds the
 //    address from an index byte, one ds_read_b32 returns the fp16 value,
-//    and one v_perm packs two of them for v_dot2.  Per element one VALU op
-//    and one LDS read plus half a v_dot2 per batch vector.  Wave w builds
+//    and one v_perm packs two of them for v_dot2.  Per element one and a
+//    half VALU ops and one LDS read, plus half a v_dot2 per batch vector.  Wave w builds
 //    entries 32 w .. 32 w + 31 of every lane's table from its 64-byte slice
 //    of the row's LUT.
 //  * NB = 1, 2, 4 or 8 vectors a pass (8 SGPRs per chunk and vector).
