@@ -86,3 +86,31 @@ def test_backend_uploads_then_synchronize(pe, gpu_ctx):
         assert np.array_equal(b.gemv(t.key, x, dim_m=t.dim_m).reshape(want.shape), want)
     b.synchronize()
     b.close()
+
+
+def test_weight_chunks_and_lifetimes(pe, gpu_ctx):
+    """Weights carved out of shared device chunks (8, 16, 32, 64 MB; over
+    16 MB a chunk of their own): freeing some, uploading more and
+    destroying the context leave every live weight's bytes intact, and
+    weights that outlive their context can still be freed."""
+    ctx = pe.Context(0)
+    shapes = [(896, 896), (4864, 896), (896, 4864), (128, 896), (1000, 2048), (151, 4000), (3, 100)] * 6
+    shapes.insert(5, (14336, 4096))  # 29.8 MB: its own chunk
+    ts = [pe.synth_tensor(N, K, 4, seed=i * 7 + N) for i, (N, K) in enumerate(shapes)]
+    ws = [ctx.upload_tensor(t) for t in ts]
+    xs = [pe.synth_x(1, t.dim_n, seed=i) for i, t in enumerate(ts)]
+    ys = [ctx.gemv(w, x) for w, x in zip(ws, xs)]
+    print(f"[chunks] {len(ws)} weights, {sum(t.payload.nbytes for t in ts) / 1e6:.1f} MB", flush=True)
+    for i in range(0, len(ws), 2):  # free every other weight
+        ws[i].free()
+    more = [ctx.upload_tensor(pe.synth_tensor(N, K, 4, seed=1000 + i)) for i, (N, K) in enumerate(shapes[:12])]
+    for i in range(1, len(ws), 2):
+        assert np.array_equal(ctx.gemv(ws[i], xs[i]), ys[i]), f"weight {i} changed"
+    half = len(ws) // 2 | 1  # an odd index: the weights still live are the odd ones
+    for i in range(1, half, 2):  # free the first chunks' remaining weights
+        ws[i].free()
+    for i in range(half, len(ws), 2):
+        assert np.array_equal(ctx.gemv(ws[i], xs[i]), ys[i]), f"weight {i} changed after chunk frees"
+    ctx.close()  # weights outlive it
+    for w in more + ws:
+        w.free()
