@@ -364,8 +364,9 @@ int weight_alloc(prism_hip_ctx* ctx, size_t bytes, uint8_t** d, WeightChunk** ch
     return PRISM_HIP_OK;
   }
   if (!ctx->carve || ctx->carve->used + need > ctx->carve->size) {
+    // at least `need`: a weight of up to kOwn bytes may exceed the next size
     WeightChunk* c = nullptr;
-    const int rc = fresh(ctx->next_chunk, &c);
+    const int rc = fresh(std::max(ctx->next_chunk, need), &c);
     if (rc) return rc;
     c->refs = 1;  // the context's
     chunk_release(ctx->carve);

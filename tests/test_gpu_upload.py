@@ -114,3 +114,29 @@ def test_weight_chunks_and_lifetimes(pe, gpu_ctx):
     ctx.close()  # weights outlive it
     for w in more + ws:
         w.free()
+
+
+@pytest.mark.parametrize("N,K,bits", [(9100, 2048, 4), (6000, 3072, 4), (10000, 896, 8)])
+def test_first_weight_larger_than_first_chunk(pe, oracle, gpu_ctx, N, K, bits):
+    """A fresh context's first weight between the first chunk size (8 MB)
+    and the own-chunk limit (16 MB) gets a chunk that holds it (it once got
+    an 8 MB chunk and was written past its end); the next small weight
+    carves after it.  Both match the oracle."""
+    ctx = pe.Context(0)
+    try:
+        t = pe.synth_tensor(N, K, bits, seed=N + K)
+        t2 = pe.synth_tensor(896, 896, 4, seed=3)
+        print(f"[first chunk] {N}x{K} {bits}-bit, {t.payload.nbytes / 1e6:.2f} MB", flush=True)
+        w = ctx.upload_tensor(t)
+        w2 = ctx.upload_tensor(t2)
+        for tt, ww in ((t, w), (t2, w2)):
+            x = pe.synth_x(1, tt.dim_n, seed=tt.dim_m)
+            y = ctx.gemv(ww, x)
+            ref = oracle.gemv(x, tt.payload, tt.dim_m, tt.dim_n, tt.bits, threads=8)
+            err = float(np.abs(y.astype(np.float32) - ref.astype(np.float32)).max() /
+                        max(np.abs(ref.astype(np.float32)).max(), 1e-30))
+            assert err <= 2e-3, f"{tt.dim_m}x{tt.dim_n}: rel_err {err:.3e}"
+        w2.free()
+        w.free()
+    finally:
+        ctx.close()
