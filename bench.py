@@ -648,7 +648,9 @@ def main() -> int:
     lpr8_static = (K // 128) in (16, 32, 64)
     if gi and bits == 8:
         nbp = 1 if batch == 1 else 2 if batch == 2 else 4 if batch <= 4 else 8
-        gemv_name = (f"k_gemv_lpr8<8,1,{nbp}>{gtag}" if batch <= (8 if lpr8_static else 4) else
+        gemv_name = (f"k_gemv_lpr8<8,1,{nbp}>{gtag}" if batch <= 4 else
+                     f"k_gemv_lpr8m{gtag}" if batch <= 8 and batch * (K // 2 + 4) <= 16512 else
+                     f"k_gemv_lpr8<8,1,{nbp}>{gtag}" if batch <= (8 if lpr8_static else 4) else
                      f"k_gemv_mfma<8,GI>{gtag}")
     elif gi:
         gemv_name = (f"k_gemv_lpr<8,1,{batch}>{gtag}" if batch <= 2 else

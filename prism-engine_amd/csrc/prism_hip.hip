@@ -700,10 +700,13 @@ void launch_lpr8(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
 }
 
 // GEMV over 8-bit GI weights: gate + up (SwiGLU, or the pair with d_y2) in
-// one k_gemv_lpr8 pass; one matrix in passes of 1 / 2 / 4 / 8 vectors
-// (k_gemv_lpr8), or of up to 16 on the matrix cores from 9 vectors on (from
-// 5 when the chunk count is not a compile-time one) (k_gemv_mfma<8, GI>).
-// x not 16-byte aligned: the generic kernel.
+// one k_gemv_lpr8 pass; one matrix in passes of 1 / 2 / 4 vectors
+// (k_gemv_lpr8), of 5..8 with the lane-per-row lookups feeding the matrix
+// cores when x fits its LDS (k_gemv_lpr8m: nb * (K / 2 + 4) <= 16512), else of 8
+// (k_gemv_lpr8), or of up to 16 on the matrix cores from 9 vectors on
+// (from 5 when the chunk count is not a compile-time one and x does not fit
+// k_gemv_lpr8m) (k_gemv_mfma<8, GI>).  x not 16-byte aligned: the generic
+// kernel.
 int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
                     uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n;
@@ -754,6 +757,16 @@ int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_h
       ga.y = y;
       ga.nb = chunk = left;
       hipLaunchKernelGGL((prism::k_gemv_generic<8, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, ga);
+    } else if (left >= 5 && left <= 8 && left * (K / 2 + prism::kLpr8mXPad) <= (uint32_t)prism::kLpr8mXDw) {
+      prism::LprArgs a{};
+      a.G = G;
+      a.w = w->d;
+      a.x = x;
+      a.y = y;
+      a.N = N;
+      a.K = K;
+      a.nb = chunk = left;
+      hipLaunchKernelGGL(prism::k_gemv_lpr8m, groups, dim3(512), 0, st, a);
     } else if (left >= 9 || (left >= 5 && !lpr8_static(K))) {
       ga.x = x;
       ga.y = y;

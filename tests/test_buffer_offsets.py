@@ -272,3 +272,81 @@ def test_gemv_lpr8_offsets(N, K):
                 perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr8 chunk")
                 assert (perf == ((lane < G) & (i < nch))).all()
                 assert ((vo + 16) <= base + gi_group_bytes(G, K, 8))[perf].all()
+
+
+LPR8M_AHEAD = _const("gemv_lpr.hpp", "kLpr8mAhead")
+LPR8M_XDW = _const("gemv_lpr.hpp", "kLpr8mXDw")
+LPR8M_XPAD = _const("gemv_lpr.hpp", "kLpr8mXPad")
+
+
+@pytest.mark.parametrize("N,K,nb", [(14336, 4096, 8), (14336, 4096, 3), (9100, 2048, 8), (16384, 2048, 5),
+                                    (8192, 2560, 8), (8192, 2560, 4)])
+def test_gemv_lpr8m_offsets(N, K, nb):
+    """k_gemv_lpr8m (gemv_lpr.hpp): wave w's 64-byte slices of the LUTs of
+    rows r and 32 + r; x in 16-byte pieces (eight per thread, past nb*K
+    nothing); double step s's chunk c0 + 2s + h of row 32t + r, or an offset
+    past the block from nd on (the loop requests AH past the end); and the
+    LDS indices of the x reads and the partials."""
+    G = gi_rows(N, K, bits=8)
+    xrow = K // 2 + LPR8M_XPAD  # LDS dwords per vector
+    assert G and nb * xrow <= LPR8M_XDW and nb <= 32, "the host's condition for this kernel"
+    assert nb * K // 8 <= 8 * 512, "x pieces: at most eight per thread"
+    Q, AH = 4, LPR8M_AHEAD
+    nd = K // (Q * 32)
+    assert nd % AH == 0, "the loop runs whole blocks of AH double steps"
+    lane = np.arange(64)
+    r32, h = lane % 32, lane // 32
+    ngroups = -(-N // G)
+    gb = gi_group_bytes(G, K, 8)
+    nbytes = ngroups * gb
+    for g in (0, ngroups - 1):
+        base = g * gb
+        for w in range(8):
+            t, q = w & 1, w >> 1
+            for rows in (r32, 32 + r32):
+                lo = np.where(rows < G, base + rows * 512 + w * 64, 0x80000000)
+                for i in range(4):
+                    perf = _check(lo + 16 * i, 0, 16, nbytes, nbytes, "gemv_lpr8m LUT")
+                    assert (perf == (rows < G)).all()
+                    assert ((lo + 16 * i + 16) <= base + (rows + 1) * 512)[perf].all(), "LUT load leaves its row"
+            row = 32 * t + r32
+            c0 = q * (K // (Q * 16))
+            ibase = np.where(row < G, base + G * 512 + ((c0 + h) * G + row) * GI_CHUNK, 0x80000000)
+            for s in range(nd + AH):
+                io = ibase + s * 2 * G * GI_CHUNK if s < nd else np.full(64, 0x80000000)
+                perf = _check(io, 0, 16, nbytes, nbytes, "gemv_lpr8m chunk")
+                assert (perf == ((row < G) & (s < nd))).all()
+                assert ((io + 16) <= base + gb)[perf].all(), "chunk load leaves its group"
+                # chunk c0 + 2s + h stays inside the wave's K quarter
+                assert (c0 + 2 * s + h < c0 + K // (Q * 16))[perf].all()
+            # x from LDS: lanes r < nb read dwords xoff + 16 s .. + 7 of their
+            # vector's row (xrow dwords, the last kLpr8mXPad of them padding)
+            xoff = r32 * xrow + 8 * (c0 + h)
+            live = r32 < nb
+            last = xoff + 16 * (nd - 1) + 8
+            assert (last[live] <= r32[live] * xrow + K // 2).all()
+            # the lanes' x elements are those of their weight bytes
+            for s in (0, nd - 1):
+                for j in (0, 1):
+                    xel = 2 * (xoff + 16 * s - r32 * xrow) + 8 * j
+                    wel = 16 * (c0 + 2 * s + h) + 8 * j
+                    assert (xel == wel).all()
+            # 16 lanes per clock for 16-byte reads: the live lanes of each
+            # 16-lane group start in distinct 4-bank groups
+            for grp in range(4):
+                ln = np.arange(16 * grp, 16 * grp + 16)
+                ln = ln[r32[ln] < nb]
+                banks = (xoff[ln] % 64) // 4
+                assert len(set(banks.tolist())) == len(ln), "x reads conflict"
+    tid = np.arange(512)
+    xq = nb * K // 8
+    for i in range(8):
+        p = tid + 512 * i
+        perf = _check(np.where(p < xq, p * 16, 0x80000000), 0, 16, nb * K * 2, nb * K * 2, "gemv_lpr8m x")
+        assert (perf == (p < xq)).all()
+    assert ((tid[:, None] + 512 * np.arange(8)[None, :]) < xq).sum() == xq, "x pieces cover x once"
+    p = np.arange(xq)
+    dst = (p // (K // 8)) * xrow + 4 * (p % (K // 8))
+    assert dst.max() + 4 <= LPR8M_XDW and len(np.unique(dst)) == xq
+    # partials: [Q][2][32][33] floats in the x region
+    assert (Q * 2 * 32 + 31) * 33 + 31 < LPR8M_XDW
