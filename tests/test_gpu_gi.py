@@ -285,8 +285,9 @@ GI8_SHAPES = [(14336, 4096), (9100, 2048), (8192, 2560), (16384, 2048)]
 @pytest.mark.parametrize("N,K", GI8_SHAPES)
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 20])
 def test_gi8_gemv(pe, oracle, gpu_ctx, N, K, batch):
-    """8-bit GI: k_gemv_lpr8 passes of 1 / 2 / 4 / 8 vectors and the
-    matrix-core GEMV over GI from 9 vectors on (from 5 with the loop form)."""
+    """8-bit GI: k_gemv_lpr8 passes of 1 / 2 / 4 vectors, k_gemv_lpr8m for
+    5..8 (lookups into the matrix cores) and the matrix-core GEMV over GI from
+    9 vectors on."""
     assert _gi(N, K, 8)
     if N * K > 4 * 10**7 and batch in (3, 5, 9):
         pytest.skip("odd batches covered at the smaller shapes")
@@ -303,8 +304,8 @@ def test_gi8_gemv(pe, oracle, gpu_ctx, N, K, batch):
 @pytest.mark.parametrize("N,K", [(14336, 4096), (8192, 2560)])
 def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     """One-hot x: every output is LUT_r[idx(r, k)] exactly, through the
-    8-bit lane-per-row GEMV at 1 and 4 vectors and the matrix-core GEMV over
-    GI (eleven vectors)."""
+    8-bit lane-per-row GEMV at 1 and 4 vectors, its matrix-core form at 8 and
+    the matrix-core GEMV over GI (eleven vectors)."""
     t = pe.synth_tensor(N, K, 8, seed=K + 13)
     lut, idx = pe.unpack_payload(t.payload, N, K, 8)
     ks = [0, 1, 15, 16, 17, K // 2 + 5, K // 3, K - 17, K - 16, K - 2, K - 1]
@@ -315,6 +316,7 @@ def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     print(f"gi8 one-hot {N}x{K}", flush=True)
     ys = gpu_ctx.gemv(w, x.view(np.uint16))
     y4 = gpu_ctx.gemv(w, x[:4].view(np.uint16))
+    y8 = gpu_ctx.gemv(w, x[:8].view(np.uint16))
     for i, k in enumerate(ks):
         want = lut[np.arange(N), idx[:, k]]
         want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
@@ -323,6 +325,25 @@ def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
         assert np.array_equal(ys[i], want), f"column {k}, eleven vectors"
         if i < 4:
             assert np.array_equal(y4[i], want), f"column {k}, four vectors"
+        if i < 8:
+            assert np.array_equal(y8[i], want), f"column {k}, eight vectors (matrix cores fed by lookups)"
+    w.free()
+
+
+@pytest.mark.parametrize("N,K,batch", [(9000, 4608, 7), (9000, 6144, 5), (9000, 6144, 6), (12000, 2048, 6),
+                                     (12000, 2048, 21)])
+def test_gi8_lpr8m_row_lengths(pe, oracle, gpu_ctx, N, K, batch):
+    """k_gemv_lpr8m at row lengths whose quarter is not a power of two
+    (K = 4608: 36 double steps per wave; 6144: 48) and at the edge of its LDS
+    (6 vectors of 6144 do not fit: the other kernels take them); 21 vectors
+    of 2048: 16 on the matrix-core GEMV over GI, then 5 on k_gemv_lpr8m."""
+    assert _gi(N, K, 8)
+    t = pe.synth_tensor(N, K, 8, seed=N + K + batch)
+    x = pe.synth_x(batch, K, seed=batch + 31)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi8 lpr8m {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    _check(y, oracle.gemv(x, t.payload, N, K, 8, threads=8), f"GI8 {N}x{K} batch {batch}")
     w.free()
 
 
