@@ -464,13 +464,20 @@ TilePlan tile_entry(int threads) {
   return p;
 }
 
+// Units per thread of the attention-combine prologue (kEpiAttnIn): at 6..8
+// the unrolled combines spilled 8..148 VGPRs, so longer rows take more waves.
+constexpr int kAttnInUplMax = 4;
+
 // x units held in VGPRs: NB * UPL * 4 registers, at most 64.
 template <int BITS, int R, bool DUAL, int NB, int EPI = 0, int WI = 1>
 TilePlan tile_pick_upl(int upl, int threads) {
   switch (upl) {
 #define PRISM_TU(u) \
   case u:           \
-    if constexpr (NB * (u) <= 16) return tile_entry<BITS, u, R, DUAL, NB, EPI, WI>(threads); else return TilePlan{};
+    if constexpr (NB * (u) <= 16 && ((EPI & prism::kEpiAttnIn) == 0 || (u) <= kAttnInUplMax)) \
+      return tile_entry<BITS, u, R, DUAL, NB, EPI, WI>(threads);                                  \
+    else                                                                                             \
+      return TilePlan{};
     PRISM_TU(1) PRISM_TU(2) PRISM_TU(3) PRISM_TU(4) PRISM_TU(5) PRISM_TU(6) PRISM_TU(7) PRISM_TU(8)
 #undef PRISM_TU
   }
@@ -489,7 +496,7 @@ TilePlan plan_tile(uint32_t bits, uint32_t N, uint32_t K, uint32_t nb, bool dual
   const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : nb <= 4 ? 4 : 8;
   if (dual && NB != 1) return TilePlan{};
   if (epi == prism::kEpiPair ? !dual : epi && (NB != 1 || bits != 4)) return TilePlan{};
-  const uint32_t uplmax = (uint32_t)(16 / NB < 8 ? 16 / NB : 8);
+  const uint32_t uplmax = (epi & prism::kEpiAttnIn) ? (uint32_t)kAttnInUplMax : (uint32_t)(16 / NB < 8 ? 16 / NB : 8);
   // Very tall single-vector 4-bit matrices (an LM head: N >= 32768) take 4
   // rows per wave: at 2 rows, dispatching N/2 workgroups costs more than
   // their bytes (measured on 151936 x 896: 47 us at R=2, 26 us at R=4), and

@@ -100,9 +100,11 @@ def test_step_long_cache_matches_oracle(gpu_ctx, n_cached):
     assert err <= STEP_TOL
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(4, 2), (4, 4), (6, 2)])
+@pytest.mark.parametrize("heads,kv_heads", [(4, 2), (4, 4), (6, 2), (40, 4)])
 def test_step_kv_widths_match_oracle(gpu_ctx, heads, kv_heads):
-    """kv_dim 128 and 256 (up to the 256 limit) and grouped heads 3:1."""
+    """kv_dim 128 and 256 (up to the 256 limit), grouped heads 3:1 and 10:1;
+    40 heads (hidden 2560) run the attention-combine O GEMV on two-wave
+    tiles (320 units per row, at most 4 per thread)."""
     cfg = pe.Qwen2Config(**{**TINY, "n_heads": heads, "n_kv_heads": kv_heads, "hidden": 64 * heads})
     m, emb_p, lay_p, kv = build(gpu_ctx, cfg, 33, 20)
     print(f"heads {heads}/{kv_heads}", flush=True)
