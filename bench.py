@@ -46,7 +46,7 @@ FP16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 1.9991 + WRITE_SIZE x 1,
 # scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_lpr_hero_4bit_b1.md
-PMC_TRAFFIC = {("hero", 1): 30113277}
+PMC_TRAFFIC = {("hero", 1): 30113735}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
