@@ -27,6 +27,12 @@ __device__ __forceinline__ uint4 ld_stream(const void* p) {
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // fp32 -> fp16, round-to-nearest-even (v_cvt_f16_f32 uses the RNE mode).
+// Buffer descriptor word 3 for gfx9-family (CDNA) raw buffers: 32-bit
+// data format, no swizzle; the range check is against num_records bytes.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy operand of the buffer-load builtins: nontemporal.
+constexpr int kNontemporal = 2;
+
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 // silu then the gate*up product with the CPU path's fp16 roundings

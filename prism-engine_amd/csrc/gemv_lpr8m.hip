@@ -1,0 +1,188 @@
+// gemv_lpr8m.hip -- k_gemv_lpr8m, built in its own translation unit with
+// the max-ilp machine scheduler (-mllvm -amdgpu-sched-strategy=max-ilp in
+// the Makefile).  That schedule suits only this kernel: config 4 at 8
+// vectors 14.50-14.61 against 15.32-15.38 us with the default scheduler,
+// while the same flag on the whole library slowed the hero GEMV (6.63-6.68
+// against 6.49-6.57 us), config 4 at 4 vectors (14.8 against 13.6), cfg2,
+// cfg1 and the decode step (542 against 529 us per token).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemv_kernels.hpp"
+#include "gemv_lpr_args.hpp"
+
+namespace prism {
+
+// 8-bit lane-per-row lookups feeding the matrix cores: the GEMV of 5..8
+// vectors over 8-bit GI weights (config 4 at batch 8), one workgroup of
+// 8 waves per group.  The lookups stay lane-private as in k_gemv_lpr8; the
+// products go to v_mfma_f32_32x32x16_f16, whose A operand is 32 weight rows
+// x 16 k (lane l: row l % 32, k 8 (l / 32) .. + 7) and whose B operand is up
+// to 32 vectors x the same 16 k, so the per-vector v_dot2 work of
+// k_gemv_lpr8 (half a v_dot2 per element and vector) becomes two MFMAs per
+// 32 elements of a row, whatever the vector count.
+//  * Waves: tile t = w & 1 holds the group's rows 32 t .. 32 t + 31, K
+//    quarter q = w >> 1 a contiguous quarter of the chunks.
+//  * Table: dword 64 b + l holds entry b of row l % 32 of tile 0 in its low
+//    half and of tile 1 in its high half (64 KB, bank-private: lane l reads
+//    bank l); one v_perm per element builds the address, one ds_read_b32
+//    returns both tiles' values and one v_perm per two elements keeps the
+//    wave's tile.
+//  * A double step covers two chunks: lane (r, h) (r = l % 32, h = l / 32)
+//    loads chunk 2 s + h of its quarter for row 32 t + r (16 bytes); MFMA j
+//    of the step takes bytes 8 j .. 8 j + 7 of that chunk, and its B operand
+//    is x[r][16 (chunk) + 8 j .. + 7].  K is permuted between the lanes'
+//    halves, identically for weights and x, so the products are the same.
+//  * x (nb * K halves, at most 64 KB) is copied to LDS once per workgroup,
+//    each vector followed by 16 bytes of padding so that the lanes r < nb,
+//    which read their vector's 16 bytes per MFMA (the others pass zeros),
+//    fall in distinct bank groups (unpadded, vectors K * 2 bytes apart all
+//    start in bank 0: bank-conflict cycles exceeded the LDS-active cycles at
+//    8 vectors).  The LDS then holds the four quarters' fp32 partials, added
+//    in quarter order.
+//  * kLpr8mAhead double steps of index bytes in flight per wave.
+// Per 32 elements of a row: 32 lookups, 48 VALU ops, 2 MFMAs.  Requires
+// K % 512 == 0, nb <= 32, nb * (K / 2 + kLpr8mXPad) <= kLpr8mXDw, 16-byte
+// aligned x and the weight block below 2 GiB.  Config 4 (14336 x 4096, 56-row groups), MI355X,
+// both kernels in one run: 8 vectors 15.0-15.2 us against 17.9-18.2 for
+// k_gemv_lpr8; 2 / 3 / 4 vectors 14.1-14.4 / 14.2-14.3 / 14.3-14.4 against
+// 12.1 / 13.5-13.6 / 13.5-13.8, so up to 4 stay with k_gemv_lpr8.  With x
+// read from global memory per MFMA 17.7 / 18.1 us at 4 / 8; 2 or 8 double
+// steps ahead, or two accumulators, no faster.
+__global__ __launch_bounds__(512) void k_gemv_lpr8m(LprArgs a) {
+  constexpr int Q = 4;  // K quarters
+  constexpr int AH = kLpr8mAhead;
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  __shared__ uint32_t lds[kLprTableDw];
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kLpr8mXDw];  // x, then the partials
+  float* red = reinterpret_cast<float*>(xs);  // [Q][2 tiles][32 vectors][33]
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t t = w & 1, q = w >> 1;
+  const uint32_t g = blockIdx.x;
+  const uint32_t N = a.N, K = a.K, G = a.G, nb = a.nb;
+  const uint32_t r32 = lane & 31, h = lane >> 5;
+  const uint32_t gbytes = gi_group_bytes(G, K, 8);
+  const uint32_t gbase = g * gbytes;
+  const __amdgpu_buffer_rsrc_t ri =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)(gridDim.x * gbytes), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(nb * K * 2u), kBufferWord3);
+
+  // ---- LUT slices (wave w: entries 32 w .. 32 w + 31 of rows r32 and
+  // 32 + r32), x, and the first index chunks
+  u32x4v L0[4], L1[4];
+  {
+    const uint32_t ra = r32, rb = 32 + r32;
+    const uint32_t la = ra < G ? gbase + gi_lut_offset(G, ra, K, 8) + w * 64u : 0x80000000u;
+    const uint32_t lb = rb < G ? gbase + gi_lut_offset(G, rb, K, 8) + w * 64u : 0x80000000u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      L0[i] = __builtin_amdgcn_raw_buffer_load_b128(ri, la + 16u * i, 0u, 0);
+      L1[i] = __builtin_amdgcn_raw_buffer_load_b128(ri, lb + 16u * i, 0u, 0);
+    }
+  }
+  const uint32_t xq = nb * K / 8;  // 16-byte pieces of x (<= 8 per thread)
+  u32x4v xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t p = tid + 512u * i;
+    xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, p < xq ? p * 16u : 0x80000000u, 0u, 0);
+  }
+  const uint32_t nd = K / (Q * 32);  // double steps per wave (a multiple of AH)
+  const uint32_t c0 = q * (K / (Q * 16));
+  const uint32_t row = 32 * t + r32;
+  const uint32_t ibase = row < G ? gbase + gi_chunk_offset(G, row, c0 + h, K, 8) : 0x80000000u;
+  const uint32_t istep = 2u * G * 16u;  // two chunks of the group
+  u32x4v ir[AH];
+  auto ld = [&](uint32_t s, int slot) {
+    ir[slot] = __builtin_amdgcn_raw_buffer_load_b128(ri, s < nd ? ibase + s * istep : 0x80000000u, 0u, kNontemporal);
+  };
+#pragma unroll
+  for (int u = 0; u < AH; u++) ld(u, u);
+
+  const uint32_t xrow = K / 2 + kLpr8mXPad;  // dwords per vector in LDS
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t p = tid + 512u * i;
+    if (p < xq) {
+      const uint32_t b = p / (K / 8), o = p % (K / 8);
+      *reinterpret_cast<u32x4v*>(&xs[b * xrow + 4 * o]) = xv[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const uint32_t e = w * 32 + 8 * i + 2 * c;
+      const uint32_t a0 = L0[i][c], a1 = L1[i][c];
+      lds[e * 64 + lane] = (a0 & 0xFFFFu) | (a1 << 16);
+      lds[(e + 1) * 64 + lane] = (a0 >> 16) | (a1 & 0xFFFF0000u);
+    }
+  __syncthreads();
+
+  const uint32_t lanebase = lane * 4u;
+  const uint32_t psel = t ? 0x07060302u : 0x05040100u;  // this tile's halves of two dwords
+  const bool xlive = r32 < nb;
+  const uint32_t xoff = r32 * xrow + 8u * (c0 + h);  // dwords: vector r32, chunk c0 + h
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+  auto step = [&](uint32_t s, int slot) {
+    u32x4v xb[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if (xlive) {
+      const u32x4v* xp = reinterpret_cast<const u32x4v*>(&xs[xoff + s * 16u]);
+      xb[0] = xp[0];
+      xb[1] = xp[1];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      uint32_t v[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t wd = ir[slot][2 * j + (i >> 2)];
+        const uint32_t ad = __builtin_amdgcn_perm(wd, lanebase, 0x0C0C0000u | ((4u + (i & 3)) << 8));
+        v[i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds) + ad);
+      }
+      u32x4v A;
+      A.x = __builtin_amdgcn_perm(v[1], v[0], psel);
+      A.y = __builtin_amdgcn_perm(v[3], v[2], psel);
+      A.z = __builtin_amdgcn_perm(v[5], v[4], psel);
+      A.w = __builtin_amdgcn_perm(v[7], v[6], psel);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, A), __builtin_bit_cast(f16x8, xb[j]), acc,
+                                                   0, 0, 0);
+    }
+  };
+  for (uint32_t s = 0; s < nd; s += AH) {
+#pragma unroll
+    for (int u = 0; u < AH; u++) {
+      step(s + u, u);
+      ld(s + u + AH, u);
+    }
+  }
+
+  // ---- D: lane (r, h) holds vector r, rows 8 (e / 4) + 4 h + e % 4 of its tile
+  __syncthreads();  // x is no longer read: the region takes the partials
+#pragma unroll
+  for (int e = 0; e < 16; e++) red[((q * 2 + t) * 32 + r32) * 33 + 8 * (e >> 2) + 4 * h + (e & 3)] = acc[e];
+  __syncthreads();
+  for (uint32_t i = tid; i < 64u * nb; i += 512) {
+    const uint32_t b = i / 64, r = i % 64;
+    const uint32_t tt = r / 32, rr = r % 32;
+    float sum = red[(tt * 32 + b) * 33 + rr];
+#pragma unroll
+    for (int v = 1; v < Q; v++) sum += red[((v * 2 + tt) * 32 + b) * 33 + rr];
+    const uint32_t grow = g * G + r;
+    if (r < G && grow < N) a.y[(size_t)b * N + grow] = f2h(sum);
+  }
+}
+
+hipError_t launch_gemv_lpr8m(dim3 groups, hipStream_t st, const LprArgs& a) {
+  hipLaunchKernelGGL(k_gemv_lpr8m, groups, dim3(512), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace prism

@@ -105,11 +105,6 @@ constexpr int kEpiResid = 2;
 constexpr int kEpiAttnIn = 4;
 constexpr int kEpiPair = 8;
 
-// Buffer descriptor word 3 for gfx9-family (CDNA) raw buffers: 32-bit
-// data format, no swizzle; the range check is against num_records bytes.
-constexpr int kBufferWord3 = 0x00020000;
-// Cache-policy operand of the buffer-load builtins: nontemporal.
-constexpr int kNontemporal = 2;
 // Index loads stream (nontemporal) except in the decode step's per-layer
 // projections (norm / residual / attention-input options, 2 rows per
 // workgroup): those weights are re-read every token, and keeping them

@@ -773,7 +773,7 @@ int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_h
       a.N = N;
       a.K = K;
       a.nb = chunk = left;
-      hipLaunchKernelGGL(prism::k_gemv_lpr8m, groups, dim3(512), 0, st, a);
+      HIP_TRY(ctx, prism::launch_gemv_lpr8m(groups, st, a));
     } else if (left >= 9 || (left >= 5 && !lpr8_static(K))) {
       ga.x = x;
       ga.y = y;

@@ -274,16 +274,16 @@ def test_gemv_lpr8_offsets(N, K):
                 assert ((vo + 16) <= base + gi_group_bytes(G, K, 8))[perf].all()
 
 
-LPR8M_AHEAD = _const("gemv_lpr.hpp", "kLpr8mAhead")
-LPR8M_XDW = _const("gemv_lpr.hpp", "kLpr8mXDw")
-LPR8M_XPAD = _const("gemv_lpr.hpp", "kLpr8mXPad")
+LPR8M_AHEAD = _const("gemv_lpr_args.hpp", "kLpr8mAhead")
+LPR8M_XDW = _const("gemv_lpr_args.hpp", "kLpr8mXDw")
+LPR8M_XPAD = _const("gemv_lpr_args.hpp", "kLpr8mXPad")
 
 
 @pytest.mark.parametrize("N,K,nb", [(14336, 4096, 8), (14336, 4096, 5), (9100, 2048, 8), (16384, 2048, 5),
                                     (8192, 2560, 8), (8192, 2560, 6), (9000, 4608, 7), (9000, 6144, 5),
                                     (12000, 2048, 6)])
 def test_gemv_lpr8m_offsets(N, K, nb):
-    """k_gemv_lpr8m (gemv_lpr.hpp): wave w's 64-byte slices of the LUTs of
+    """k_gemv_lpr8m (gemv_lpr8m.hip): wave w's 64-byte slices of the LUTs of
     rows r and 32 + r; x in 16-byte pieces (eight per thread, past nb*K
     nothing); double step s's chunk c0 + 2s + h of row 32t + r, or an offset
     past the block from nd on (the loop requests AH past the end); and the
