@@ -45,8 +45,10 @@ HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 # HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 1.9991 + WRITE_SIZE x 1,
-# scales from a 64 MiB copy), by (workload, batch): profiles/k_gemv_lpr_hero_4bit_b1.md
-PMC_TRAFFIC = {("hero", 1): 30113735}
+# scales from a 64 MiB copy), by (workload, batch): (bytes, the kernel the profile
+# measured, the profile).  A line carries the figure only when the library reports
+# that the same kernel ran.
+PMC_TRAFFIC = {("hero", 1): (30113735, "k_gemv_lpr<8, 1, 1, 0, 16>", "profiles/k_gemv_lpr_hero_4bit_b1.md")}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)
@@ -84,17 +86,6 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def gi_rows(bits: int, N: int, K: int, num_cu: int) -> int:
-    """The library's device-layout rule (prism_hip.hip gi_rows): matrices
-    with K >= 2048 (4-bit: K % 64 == 0; 8-bit: K % 512 == 0) whose rows fill
-    every CU in one round of 32..64-row groups are regrouped to the GI layout
-    (G rows per group) and run on the lane-per-row GEMVs.  Returns G, or 0."""
-    if K < 2048 or bits not in (4, 8) or K % (64 if bits == 4 else 512):
-        return 0
-    G = (-(-N // num_cu) + 7) // 8 * 8
-    return G if 32 <= G <= 64 else 0
-
-
 def weight_bytes(bits: int, N: int, K: int) -> int:
     return N * (2 << bits) + N * (K // 2 if bits == 4 else K)
 
@@ -116,6 +107,68 @@ class _pinned_core:
     def __exit__(self, *a):
         if self.old is not None:
             os.sched_setaffinity(0, self.old)
+
+
+def device_busy(stream, ms: float = 2.0) -> None:
+    """Enqueue a bounded spin of about `ms` on `stream`, so that the work
+    recorded after it (an event, a graph) is submitted while the GPU is busy
+    and the timed region holds device work only, not the host's submission
+    latency.  The spin's cycles-per-ms is measured on first use."""
+    import torch
+    global _SPIN_CYCLES_PER_MS
+    if _SPIN_CYCLES_PER_MS is None:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(1 << 18)  # warm
+            a.record(stream)
+            torch.cuda._sleep(1 << 20)
+            b.record(stream)
+        torch.cuda.synchronize()
+        _SPIN_CYCLES_PER_MS = (1 << 20) / max(a.elapsed_time(b), 1e-3)
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(int(ms * _SPIN_CYCLES_PER_MS))
+
+
+_SPIN_CYCLES_PER_MS = None
+
+
+def time_launches(launch, steps: int, warmup: int, stream, use_graph: bool):
+    """Warm up, then time exactly `steps` launches (captured into one HIP
+    graph and replayed, or issued eagerly) with events on `stream`, behind a
+    device-side spin (device_busy).  Returns (device ms, wall ms)."""
+    import torch
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            launch(i)
+    torch.cuda.synchronize()
+    graph = None
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                launch(i)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()  # untimed first replay (graph upload)
+        torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    device_busy(stream)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        if graph is not None:
+            graph.replay()
+        else:
+            for i in range(steps):
+                launch(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    del graph
+    return e0.elapsed_time(e1), wall * 1e3
 
 
 def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
@@ -214,6 +267,7 @@ def run_decode(args, pe, seed) -> int:
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
+    device_busy(stream)
     e0.record(stream)
     for i in range(args.steps):
         step(i)
@@ -475,6 +529,7 @@ def main() -> int:
                     help="batch for gemv workloads (cfg4 sweep), rows of X (M) for the GEMM")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-floor", action="store_true", help="skip the same-process read-floor leg")
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes the steps rotate over")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="after timing, run one untimed device copy of MB MiB (scale reference for "
@@ -569,41 +624,34 @@ def main() -> int:
             log("[bench] PARITY FAILURE")
             return 1
 
-    with torch.cuda.stream(stream):
-        for i in range(args.warmup):
-            launch(i)
-    torch.cuda.synchronize()
-    log(f"[bench] warmup {args.warmup} done")
+    # the kernels the library's dispatch picked for one step, as it reports them
+    kernel_name = ctx.last_kernels()
+    log(f"[bench] kernels of one step: {kernel_name}")
 
-    graph = None
-    if not args.no_graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(args.steps):
-                launch(i)
-        torch.cuda.synchronize()
-        with torch.cuda.stream(stream):
-            graph.replay()  # untimed first replay (graph upload)
-        torch.cuda.synchronize()
-        log(f"[bench] captured {args.steps} launches into a HIP graph")
-
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_wall = time.perf_counter()
-    with torch.cuda.stream(stream):
-        e0.record(stream)
-        if graph is not None:
-            graph.replay()
-        else:
-            for i in range(args.steps):
-                launch(i)
-        e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
-    ms = e0.elapsed_time(e1)
+    ms, wall_ms = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph)
     ms_step = ms / args.steps
-    log(f"[bench] timed {args.steps} steps: {ms:.3f} ms on device events, {wall * 1e3:.3f} ms wall")
+    launch_mode = "eager" if args.no_graph else "hip_graph"
+    log(f"[bench] timed {args.steps} steps ({launch_mode}, behind a device-side spin): {ms:.3f} ms on device "
+        f"events, {wall_ms:.3f} ms wall")
+
+    # the read floor in the same process: k_stream_read over as many bytes
+    # per launch, rotated over as many distinct buffers, timed the same way
+    floor = None
+    if kind in ("gemv", "gateup") and not args.no_floor:
+        g = torch.Generator(device=dev).manual_seed(seed + 1)
+        fbufs = [torch.randint(0, 256, (wb,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
+        fsink = torch.zeros(256, dtype=torch.int32, device=dev)
+
+        def flaunch(i: int) -> None:
+            ctx.stream_read_dev(fbufs[i % copies], wb, fsink, stream)
+        fms, _ = time_launches(flaunch, args.steps, args.warmup, stream, not args.no_graph)
+        f_us = fms / args.steps * 1e3
+        floor = {"kernel": "k_stream_read", "us_per_launch": round(f_us, 4),
+                 "GBps": round(wb / (f_us * 1e-6) / 1e9, 2), "kernel_over_floor": round(ms_step * 1e3 / f_us, 4),
+                 "bytes_per_launch": wb, "buffers_rotated": copies}
+        log(f"[bench] read floor (same process, same bytes and rotation): {f_us:.3f} us per launch; "
+            f"this workload takes {floor['kernel_over_floor']:.3f} x the floor")
+        del fbufs, fsink
 
     if args.copy_calibration > 0:
         src = torch.empty(args.copy_calibration << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -629,43 +677,11 @@ def main() -> int:
                   if kind == "floor" else
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": PMC_TRAFFIC.get((args.workload, batch))}
-    # the library's GEMV dispatch: 5..16 vectors (4-bit rows up to 8192 long:
-    # 3..16, and 2 over >= 8192 rows) over >= 4096 rows run on the matrix cores
-    mfma = (kind == "gemv" and N >= 4096 and K % 128 == 0 and
-            (5 <= batch <= 16 or (bits == 4 and K <= 8192 and (3 <= batch <= 4 or (batch == 2 and N >= 8192)))))
-    # and its GEMM dispatch: prefills of up to 256 rows split K over one
-    # 128- or 256-row block (at most 4 splits, at least 8 K steps each)
-    gi = gi_rows(bits, N, K, torch.cuda.get_device_properties(0).multi_processor_count)
-    gtag = f" (GI{gi})" if gi else ""
-    gemm4 = f"k_gemm_w4<{2 if batch <= 256 else 4 if batch <= 512 else 8}>" + gtag
-    if bits == 4 and batch <= 256:
-        smi = 4 if batch <= 128 else 8
-        blocks = -(-batch // (32 * smi)) * -(-N // 256)
-        sk = min(4, 256 // blocks, (K // 64) // 8)
-        if sk >= 2:
-            gemm4 = f"k_gemm_w4<{smi}>{gtag} in {sk} K splits + k_gemm_split_sum"
-    lpr8_static = (K // 128) in (16, 32, 64)
-    if gi and bits == 8:
-        nbp = 1 if batch == 1 else 2 if batch == 2 else 4 if batch <= 4 else 8
-        gemv_name = (f"k_gemv_lpr8<8,1,{nbp}>{gtag}" if batch <= 4 else
-                     f"k_gemv_lpr8m{gtag}" if batch <= 8 and batch * (K // 2 + 4) <= 16512 else
-                     f"k_gemv_lpr8<8,1,{nbp}>{gtag}" if batch <= (8 if lpr8_static else 4) else
-                     f"k_gemv_mfma<8,GI>{gtag}")
-    elif gi:
-        gemv_name = (f"k_gemv_lpr<8,1,{batch}>{gtag}" if batch <= 2 else
-                     f"k_gemv_mfma<4,GI>{gtag}" if K % 128 == 0 else f"k_gemv_lpr<8,1,2> passes{gtag}")
-    else:
-        gemv_name = f"k_gemv_mfma<{bits}>" if mfma else "k_gemv_tile"
-    kernel_name = {"floor": "k_stream_read", "gemv": gemv_name,
-                   "gateup": ((f"k_gemv_lpr8<8,2,1,SwiGLU>{gtag}" if bits == 8 else f"k_gemv_lpr<16,2,1,SwiGLU>{gtag}")
-                              if gi else "k_gemv_tile (DUAL gate_up + SwiGLU)"),
-                   "gemm": ("GEMV passes" if batch <= (48 if bits == 8 else 32) else
-                            gemm4 if bits == 4 else
-                            f"k_gemm8{gtag}" if (batch > 256 or gi) and K % 64 == 0 and
-                            not (batch <= 256 and min(4, 256 // -(-N // 128), (K // 64) // 8) >= 2) else
-                            f"k_gemm8 in {min(4, 256 // -(-N // 128), (K // 64) // 8)} K splits + k_gemm_split_sum"
-                            if K % 64 == 0 and min(4, 256 // -(-N // 128), (K // 64) // 8) >= 2 else "k_gemm<8>")}[kind]
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None}
+        pmc = PMC_TRAFFIC.get((args.workload, batch))
+        if pmc is not None and pmc[1] == kernel_name:
+            roof["traffic"] = pmc[0]
+            roof["traffic_source"] = f"{pmc[2]} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of {pmc[1]})"
     roof["kernel"] = kernel_name
     roof["algorithmic_per_launch"] = (2.0 * batch * N * K) if kind == "gemm" else wb
 
@@ -692,8 +708,9 @@ def main() -> int:
                  "synthetic (seeded PCG64: x~N(0,1) fp16, uniform indices, sorted N(0,0.02) fp16 LUTs)"),
         "config": {"workload": args.workload, "kind": kind, "bits": bits, "N": N, "K": K,
                    ("M" if kind == "gemm" else "batch"): batch, "weight_copies_rotated": copies,
-                   "launch": "hip_graph" if graph is not None else "eager", "seed": seed},
+                   "launch": launch_mode, "seed": seed},
         "roofline": roof,
+        "floor": floor,
         "cpu_baseline": cpu,
         "parity_rel_err": err,
     }

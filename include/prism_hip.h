@@ -305,6 +305,16 @@ const void* prism_hip_model_logits_dev(const prism_hip_model* m);
  * `stream` (NULL: the context stream) and returns. */
 int prism_hip_stream_read_dev(prism_hip_ctx* ctx, const void* d_buf, size_t bytes, void* d_sink, void* stream);
 
+/* The kernels the dispatch launched in the context's most recent compute
+ * call (GEMV, gate/up, GEMM, row decode, palettize, read floor), by their
+ * device names in launch order, joined by " + ", e.g.
+ * "k_gemv_lpr<8, 1, 1, 0, 16>"; a kernel launched n > 1 times in a row
+ * appears once followed by " x<n>" ("k_gemv_mfma<4, true> x3").  "" before the
+ * first such call.  No counterpart in the reference: measurement and tests
+ * read it to label what ran.  The pointer stays valid until the next call
+ * on the context. */
+const char* prism_hip_last_kernels(prism_hip_ctx* ctx);
+
 #ifdef __cplusplus
 }
 #endif

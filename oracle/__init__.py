@@ -60,12 +60,15 @@ from __future__ import annotations
 import ctypes
 import os
 import subprocess
+import threading
 
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "libprism_cpuref.so")
 _lib = None
+# serialises calls that switch the C library's fold mode (cpuref_set_fold_mode)
+FOLD_LOCK = threading.Lock()
 
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
@@ -136,6 +139,8 @@ def lib():
         L.cpuref_decode_step.restype = ctypes.c_int
         L.cpuref_set_fold_mode.argtypes = [ctypes.c_int]
         L.cpuref_set_fold_mode.restype = None
+        L.cpuref_fold_overflowed.argtypes = []
+        L.cpuref_fold_overflowed.restype = ctypes.c_int
         _f32p = ctypes.POINTER(ctypes.c_float)
         L.cpuref_fit_palette.argtypes = [_f32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _f32p]
         L.cpuref_fit_palette.restype = ctypes.c_size_t
@@ -381,12 +386,18 @@ def decode_step(dims, eps: float, embed, layers, kv: KVState, token: int, pos: i
     embed = np.ascontiguousarray(embed, dtype=np.uint8)
     logits = np.zeros(int(dims[6]), dtype=np.uint16)
     L_ = lib()
-    L_.cpuref_set_fold_mode(int(fold))
-    try:
-        rc = L_.cpuref_decode_step(d, ctypes.c_float(eps), _p8(embed), wp, kp, vp, lens, token, pos,
-                                   _p16(logits), threads)
-    finally:
-        L_.cpuref_set_fold_mode(0)
+    # the fold mode is a process-wide switch of the C library: one call at a
+    # time holds it
+    with FOLD_LOCK:
+        L_.cpuref_set_fold_mode(int(fold))
+        try:
+            rc = L_.cpuref_decode_step(d, ctypes.c_float(eps), _p8(embed), wp, kp, vp, lens, token, pos,
+                                       _p16(logits), threads)
+        finally:
+            L_.cpuref_set_fold_mode(0)
+            overflow = L_.cpuref_fold_overflowed()
+    if overflow:
+        raise ValueError("fold mode 1: a sum of more than 131072 terms (2048 blocks of 64) has no blocked order here")
     assert rc == 0, rc
     for l in range(L):
         kv.len[l] = lens[l]

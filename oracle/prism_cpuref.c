@@ -115,6 +115,16 @@ uint16_t cpuref_f32_to_f16(float f) {
 int cpuref_fold_mode = 0;
 void cpuref_set_fold_mode(int mode) { cpuref_fold_mode = mode; }
 
+/* Set when a blocked sum had more than 2048 blocks (131072 terms): mode 1
+ * then refuses to give a result rather than drop terms; the caller reads
+ * and clears it (cpuref_fold_overflowed). */
+static volatile int cpuref_fold_overflow = 0;
+int cpuref_fold_overflowed(void) {
+  const int v = cpuref_fold_overflow;
+  cpuref_fold_overflow = 0;
+  return v;
+}
+
 /* Blocked accumulator for mode 1: add terms in order, close a block every
  * 64 terms, and finish with a pairwise tree over the block sums. */
 typedef struct {
@@ -130,13 +140,21 @@ void cpuref_blocked_init(cpuref_blocked* b) {
 void cpuref_blocked_add(cpuref_blocked* b, float v) {
   b->acc += v;
   if (++b->cnt == 64) {
-    if (b->nparts < 2048) b->part[b->nparts++] = b->acc;
+    if (b->nparts < 2048)
+      b->part[b->nparts++] = b->acc;
+    else
+      cpuref_fold_overflow = 1;
     b->acc = 0.0f;
     b->cnt = 0;
   }
 }
 float cpuref_blocked_sum(cpuref_blocked* b) {
-  if (b->cnt && b->nparts < 2048) b->part[b->nparts++] = b->acc;
+  if (b->cnt) {
+    if (b->nparts < 2048)
+      b->part[b->nparts++] = b->acc;
+    else
+      cpuref_fold_overflow = 1;
+  }
   size_t n = b->nparts;
   if (n == 0) return 0.0f;
   while (n > 1) {

@@ -62,6 +62,11 @@ class Context:
         if rc != _native.OK:
             raise PrismHipError(rc, self.error())
 
+    def last_kernels(self) -> str:
+        """The kernels the dispatch launched in this context's most recent
+        compute call, e.g. "k_gemv_lpr<8, 1, 1, 0, 16>" (prism_hip_last_kernels)."""
+        return self.lib.prism_hip_last_kernels(self.h).decode()
+
     def upload(self, payload: np.ndarray, dim_m: int, dim_n: int, bits: int) -> "Weight":
         payload = np.ascontiguousarray(payload, dtype=np.uint8)
         h = self.lib.prism_hip_weight_upload(self.h, payload.ctypes.data, payload.size, dim_m, dim_n, bits,

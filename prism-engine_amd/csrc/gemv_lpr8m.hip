@@ -181,6 +181,7 @@ __global__ __launch_bounds__(512) void k_gemv_lpr8m(LprArgs a) {
 }
 
 hipError_t launch_gemv_lpr8m(dim3 groups, hipStream_t st, const LprArgs& a) {
+  note_launch(reinterpret_cast<const void*>(&k_gemv_lpr8m));
   hipLaunchKernelGGL(k_gemv_lpr8m, groups, dim3(512), 0, st, a);
   return hipGetLastError();
 }

@@ -26,4 +26,8 @@ constexpr int kLpr8mAhead = 4;
 constexpr int kLpr8mXPad = 4;       // dwords after each vector of x in LDS
 constexpr int kLpr8mXDw = 16512;  // LDS dwords for x: nb * (K / 2 + kLpr8mXPad) <= kLpr8mXDw
 
+// Records a launched kernel (by host function) in the launch log of the
+// compute call running on this thread, if any (prism_hip.hip).
+void note_launch(const void* fn);
+
 }  // namespace prism

@@ -7,6 +7,7 @@
 // CPU fallback: every failure is returned as a negative code with text.
 #include "prism_hip.h"
 
+#include <cxxabi.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -14,6 +15,7 @@
 #include <condition_variable>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -59,7 +61,8 @@ struct prism_hip_ctx {
   // created on first use; it keeps what it has allocated, so a call after
   // the first reuses memory instead of allocating.
   hipMemPool_t pool = nullptr;
-  // This device's address of the static split-K scratch (set at create).
+  // This device's address of the static split-K scratch (looked up on the
+  // first prism_hip_gemm_dev_noalloc).
   float* scratch = nullptr;
   // Host uploads: a ring of pinned staging buffers (created on first use),
   // each with the event of the last copy out of it, and a device buffer for
@@ -81,6 +84,48 @@ struct prism_hip_ctx {
   std::unordered_set<prism_hip_weight*> weights;
   // Decode-step models created on this context, orphaned the same way.
   std::unordered_set<prism_hip_model*> models;
+  // Host functions of the kernels the last compute call launched, in
+  // order, and their names once asked for (prism_hip_last_kernels).
+  std::vector<const void*> launched;
+  std::string kernels;
+};
+
+namespace prism {
+
+// The launch log of the compute call running on this thread (NULL outside
+// one): every dispatch site appends the kernel it launches.
+thread_local std::vector<const void*>* g_launch_log = nullptr;
+
+void note_launch(const void* fn) {
+  if (g_launch_log) g_launch_log->push_back(fn);
+}
+
+}  // namespace prism
+
+// hipLaunchKernelGGL that records the kernel (KERNEL as for
+// hipLaunchKernelGGL: a template-id in parentheses).
+#define PRISM_LAUNCH(KERNEL, ...)                                 \
+  do {                                                            \
+    prism::note_launch(reinterpret_cast<const void*>(&KERNEL));   \
+    hipLaunchKernelGGL(KERNEL, __VA_ARGS__);                      \
+  } while (0)
+
+// hipLaunchKernel that records the kernel.
+static hipError_t launch_fn(const void* fn, dim3 grid, dim3 block, void** args, size_t lds, hipStream_t st) {
+  prism::note_launch(fn);
+  return hipLaunchKernel(fn, grid, block, args, lds, st);
+}
+
+// For the length of one compute call: clears the context's launch log and
+// makes it the thread's.
+struct LaunchLog {
+  std::vector<const void*>* prev;
+  explicit LaunchLog(prism_hip_ctx* ctx) : prev(prism::g_launch_log) {
+    ctx->launched.clear();
+    ctx->kernels.clear();
+    prism::g_launch_log = &ctx->launched;
+  }
+  ~LaunchLog() { prism::g_launch_log = prev; }
 };
 
 // Defined with prism_hip_model (model_step.hpp): forget the context.
@@ -117,22 +162,17 @@ namespace {
 
 thread_local std::string g_create_err;
 
-// This device's address of `scratch` (the device is current).
+// This device's address of `scratch` (the device is current), looked up
+// once per device on the first no-alloc call that needs it.
 hipError_t device_scratch(int device, float** out) {
   static std::mutex mu;
   static float* addr[64] = {};
-  if (device < 0 || device >= 64) {
-    g_create_err = "device index out of range";
-    return hipErrorInvalidDevice;
-  }
+  if (device < 0 || device >= 64) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(mu);
   if (!addr[device]) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess) {
-      g_create_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
-      return e;
-    }
+    if (e != hipSuccess) return e;
     addr[device] = static_cast<float*>(p);
   }
   *out = addr[device];
@@ -625,7 +665,7 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
       a.nb = chunk;
       const void* fn = bits == 8 ? reinterpret_cast<const void*>(&prism::k_gemv_mfma<8>)
                                  : reinterpret_cast<const void*>(&prism::k_gemv_mfma<4>);
-      HIP_TRY(ctx, hipLaunchKernel(fn, dim3((N + prism::kGmRows - 1) / prism::kGmRows), dim3(64 * prism::kGmWaves),
+      HIP_TRY(ctx, launch_fn(fn, dim3((N + prism::kGmRows - 1) / prism::kGmRows), dim3(64 * prism::kGmWaves),
                                    args, 0, st));
       b0 += chunk;
       continue;
@@ -646,7 +686,7 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
     a.nb = chunk;
     if (p.fn) {
       const uint32_t grid = (N + (uint32_t)p.R - 1) / (uint32_t)p.R;
-      HIP_TRY(ctx, hipLaunchKernel(p.fn, dim3(grid), dim3(p.threads), args, p.lds, st));
+      HIP_TRY(ctx, launch_fn(p.fn, dim3(grid), dim3(p.threads), args, p.lds, st));
     } else {
       if (epi && !pair) return fail(ctx, PRISM_HIP_ERR_SHAPE, "no fused kernel for %u-bit %ux%u", bits, N, K);
       const void* fn;
@@ -659,7 +699,7 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
       else
         fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemv_generic<4, prism::kGenSingle>)
                        : reinterpret_cast<const void*>(&prism::k_gemv_generic<8, prism::kGenSingle>);
-      HIP_TRY(ctx, hipLaunchKernel(fn, dim3(N), dim3(64), args, 0, st));
+      HIP_TRY(ctx, launch_fn(fn, dim3(N), dim3(64), args, 0, st));
     }
     b0 += chunk;
   }
@@ -678,11 +718,11 @@ void launch_lpr(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
   const uint32_t NC = a.K / 32;
   const uint32_t nch = NC % S == 0 ? NC / S : 0;
   if (nch == 16)
-    hipLaunchKernelGGL((prism::k_gemv_lpr<S, NM, NB, EPI, 16>), groups, dim3(64 * S), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI, 16>), groups, dim3(64 * S), 0, st, a);
   else if (nch == 8)
-    hipLaunchKernelGGL((prism::k_gemv_lpr<S, NM, NB, EPI, 8>), groups, dim3(64 * S), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI, 8>), groups, dim3(64 * S), 0, st, a);
   else
-    hipLaunchKernelGGL((prism::k_gemv_lpr<S, NM, NB, EPI>), groups, dim3(64 * S), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI>), groups, dim3(64 * S), 0, st, a);
 }
 
 // 8-bit GI weights: k_gemv_lpr8 with the wave's chunk count as a
@@ -693,17 +733,23 @@ bool lpr8_static(uint32_t K) {
   const uint32_t nch = K / 16 / 8;
   return nch == 16 || nch == 32 || nch == 64;
 }
+// Eight vectors with a run-time chunk count have no kernel: that returns an
+// error (the dispatch below never asks for it) instead of launching nothing.
 template <int NM, int NB, int EPI>
-void launch_lpr8(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
+int launch_lpr8(prism_hip_ctx* ctx, dim3 groups, hipStream_t st, const prism::LprArgs& a) {
   const uint32_t nch = a.K / 16 / 8;
   if (nch == 32)
-    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI, 32>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 32>), groups, dim3(512), 0, st, a);
   else if (nch == 16)
-    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI, 16>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 16>), groups, dim3(512), 0, st, a);
   else if (nch == 64)
-    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI, 64>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 64>), groups, dim3(512), 0, st, a);
   else if constexpr (NB < 8)
-    hipLaunchKernelGGL((prism::k_gemv_lpr8<8, NM, NB, EPI>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI>), groups, dim3(512), 0, st, a);
+  else
+    return fail(ctx, PRISM_HIP_ERR_SHAPE, "k_gemv_lpr8: %d vectors need a compile-time chunk count (K = %u)", NB,
+                a.K);
+  return PRISM_HIP_OK;
 }
 
 // GEMV over 8-bit GI weights: gate + up (SwiGLU, or the pair with d_y2) in
@@ -742,14 +788,13 @@ int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_h
       a.N = N;
       a.K = K;
       a.nb = 1;
-      if (d_y2)
-        launch_lpr8<2, 1, prism::kLprPair>(groups, st, a);
-      else
-        launch_lpr8<2, 1, prism::kLprSwiglu>(groups, st, a);
+      const int rc = d_y2 ? launch_lpr8<2, 1, prism::kLprPair>(ctx, groups, st, a)
+                          : launch_lpr8<2, 1, prism::kLprSwiglu>(ctx, groups, st, a);
+      if (rc) return rc;
     } else if (d_y2) {
-      hipLaunchKernelGGL((prism::k_gemv_generic<8, prism::kGenPair, true>), dim3(N), dim3(64), 0, st, ga);
+      PRISM_LAUNCH((prism::k_gemv_generic<8, prism::kGenPair, true>), dim3(N), dim3(64), 0, st, ga);
     } else {
-      hipLaunchKernelGGL((prism::k_gemv_generic<8, prism::kGenSwiglu, true>), dim3(N), dim3(64), 0, st, ga);
+      PRISM_LAUNCH((prism::k_gemv_generic<8, prism::kGenSwiglu, true>), dim3(N), dim3(64), 0, st, ga);
     }
     HIP_TRY(ctx, hipGetLastError());
     return PRISM_HIP_OK;
@@ -763,7 +808,7 @@ int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_h
       ga.x = x;
       ga.y = y;
       ga.nb = chunk = left;
-      hipLaunchKernelGGL((prism::k_gemv_generic<8, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, ga);
+      PRISM_LAUNCH((prism::k_gemv_generic<8, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, ga);
     } else if (left >= 5 && left <= 8 && left * (K / 2 + prism::kLpr8mXPad) <= (uint32_t)prism::kLpr8mXDw) {
       prism::LprArgs a{};
       a.G = G;
@@ -778,8 +823,8 @@ int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_h
       ga.x = x;
       ga.y = y;
       ga.nb = chunk = left < (uint32_t)prism::kGmMaxNb ? left : (uint32_t)prism::kGmMaxNb;
-      hipLaunchKernelGGL((prism::k_gemv_mfma<8, true>), dim3((N + prism::kGmRows - 1) / prism::kGmRows),
-                         dim3(64 * prism::kGmWaves), 0, st, ga);
+      PRISM_LAUNCH((prism::k_gemv_mfma<8, true>), dim3((N + prism::kGmRows - 1) / prism::kGmRows),
+                   dim3(64 * prism::kGmWaves), 0, st, ga);
     } else {
       prism::LprArgs a{};
       a.G = G;
@@ -789,14 +834,11 @@ int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_h
       a.N = N;
       a.K = K;
       a.nb = chunk = left;
-      if (left == 1)
-        launch_lpr8<1, 1, prism::kLprPlain>(groups, st, a);
-      else if (left == 2)
-        launch_lpr8<1, 2, prism::kLprPlain>(groups, st, a);
-      else if (left <= 4)
-        launch_lpr8<1, 4, prism::kLprPlain>(groups, st, a);
-      else
-        launch_lpr8<1, 8, prism::kLprPlain>(groups, st, a);
+      const int rc = left == 1   ? launch_lpr8<1, 1, prism::kLprPlain>(ctx, groups, st, a)
+                     : left == 2 ? launch_lpr8<1, 2, prism::kLprPlain>(ctx, groups, st, a)
+                     : left <= 4 ? launch_lpr8<1, 4, prism::kLprPlain>(ctx, groups, st, a)
+                                 : launch_lpr8<1, 8, prism::kLprPlain>(ctx, groups, st, a);
+      if (rc) return rc;
     }
     HIP_TRY(ctx, hipGetLastError());
     b0 += chunk;
@@ -841,9 +883,9 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.K = K;
       a.nb = 1;
       if (d_y2)
-        hipLaunchKernelGGL((prism::k_gemv_generic<4, prism::kGenPair, true>), dim3(N), dim3(64), 0, st, a);
+        PRISM_LAUNCH((prism::k_gemv_generic<4, prism::kGenPair, true>), dim3(N), dim3(64), 0, st, a);
       else
-        hipLaunchKernelGGL((prism::k_gemv_generic<4, prism::kGenSwiglu, true>), dim3(N), dim3(64), 0, st, a);
+        PRISM_LAUNCH((prism::k_gemv_generic<4, prism::kGenSwiglu, true>), dim3(N), dim3(64), 0, st, a);
     }
     HIP_TRY(ctx, hipGetLastError());
     return PRISM_HIP_OK;
@@ -862,7 +904,7 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.N = N;
       a.K = K;
       a.nb = chunk = left;
-      hipLaunchKernelGGL((prism::k_gemv_generic<4, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, a);
+      PRISM_LAUNCH((prism::k_gemv_generic<4, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, a);
     } else if (left >= 3 && K % prism::kGmGroup == 0) {
       prism::GemvArgs a{};
       a.gi = G;
@@ -872,8 +914,8 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.N = N;
       a.K = K;
       a.nb = chunk = left < (uint32_t)prism::kGmMaxNb ? left : (uint32_t)prism::kGmMaxNb;
-      hipLaunchKernelGGL((prism::k_gemv_mfma<4, true>), dim3((N + prism::kGmRows - 1) / prism::kGmRows),
-                         dim3(64 * prism::kGmWaves), 0, st, a);
+      PRISM_LAUNCH((prism::k_gemv_mfma<4, true>), dim3((N + prism::kGmRows - 1) / prism::kGmRows),
+                   dim3(64 * prism::kGmWaves), 0, st, a);
     } else {
       prism::LprArgs a{};
       a.G = G;
@@ -936,10 +978,10 @@ int launch_gemm_blocks(prism_hip_ctx* ctx, const void* fn, uint32_t tiles, uint3
   }
   uint32_t G = w->gi;  // GI group rows (0: split-block; k_gemm8 ignores it)
   void* args[] = {&lut, &idx, &X, &Y, &M, &N, &K, &P, &kps, &G};
-  hipError_t e = hipLaunchKernel(fn, dim3(tiles, ns), dim3(256), args, 0, st);
+  hipError_t e = launch_fn(fn, dim3(tiles, ns), dim3(256), args, 0, st);
   if (e == hipSuccess && split) {
     const uint64_t mn = (uint64_t)M * N;
-    hipLaunchKernelGGL(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y, mn, ns);
+    PRISM_LAUNCH(prism::k_gemm_split_sum, dim3((unsigned)((mn + 1023) / 1024)), dim3(256), 0, st, P, Y, mn, ns);
     e = hipGetLastError();
   }
   if (split && !fixed) {
@@ -1044,7 +1086,7 @@ int launch_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const void* d_X, 
   void* args[] = {&lut, &idx, &X, &Y, &M, const_cast<uint32_t*>(&N), const_cast<uint32_t*>(&K)};
   const void* fn = bits == 4 ? reinterpret_cast<const void*>(&prism::k_gemm<4>)
                              : reinterpret_cast<const void*>(&prism::k_gemm<8>);
-  HIP_TRY(ctx, hipLaunchKernel(fn, dim3(tiles), dim3(256), args, 0, st));
+  HIP_TRY(ctx, launch_fn(fn, dim3(tiles), dim3(256), args, 0, st));
   return PRISM_HIP_OK;
 }
 
@@ -1064,7 +1106,7 @@ int launch_decode(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t row0, 
                                         : reinterpret_cast<const void*>(&prism::k_decode_rows<8>))
                    : w->gi      ? reinterpret_cast<const void*>(&prism::k_decode_rows<4, true>)
                                 : reinterpret_cast<const void*>(&prism::k_decode_rows<4>);
-  HIP_TRY(ctx, hipLaunchKernel(fn, dim3((unsigned)blocks), dim3(256), args, 0, st));
+  HIP_TRY(ctx, launch_fn(fn, dim3((unsigned)blocks), dim3(256), args, 0, st));
   return PRISM_HIP_OK;
 }
 
@@ -1081,7 +1123,7 @@ int copy_split_rows(prism_hip_ctx* ctx, const prism_hip_weight* w, uint8_t* dst_
   }
   const size_t pieces = (size_t)N * (2 + K / 32);
   const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
-  hipLaunchKernelGGL(prism::k_gi_unpack, dim3(grid), dim3(256), 0, st, w->d, dst_lut, dst_idx, N, K, w->gi);
+  PRISM_LAUNCH(prism::k_gi_unpack, dim3(grid), dim3(256), 0, st, w->d, dst_lut, dst_idx, N, K, w->gi);
   HIP_TRY(ctx, hipGetLastError());
   return PRISM_HIP_OK;
 }
@@ -1116,11 +1158,8 @@ prism_hip_ctx* prism_hip_ctx_create(int device) {
     g_create_err = std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950";
     return nullptr;
   }
-  float* scratch = nullptr;
-  if (device_scratch(device, &scratch) != hipSuccess) return nullptr;
   auto* ctx = new prism_hip_ctx;
   ctx->device = device;
-  ctx->scratch = scratch;
   ctx->num_cu = prop.multiProcessorCount;
   ctx->lds_max = prop.sharedMemPerBlock;
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
@@ -1159,6 +1198,49 @@ void prism_hip_ctx_destroy(prism_hip_ctx* ctx) {
 
 const char* prism_hip_last_error(const prism_hip_ctx* ctx) {
   return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+const char* prism_hip_last_kernels(prism_hip_ctx* ctx) {
+  if (!ctx) return "";
+  if (ctx->kernels.empty() && !ctx->launched.empty()) {
+    // device names of the recorded host functions, demangled and shortened
+    // to the kernel's own name and template arguments
+    std::string out, prev;
+    int run = 0;
+    auto flush = [&] {
+      if (prev.empty()) return;
+      if (!out.empty()) out += " + ";
+      out += prev;
+      if (run > 1) out += " x" + std::to_string(run);
+    };
+    for (const void* fn : ctx->launched) {
+      const char* raw = hipKernelNameRefByPtr(fn, ctx->stream);
+      std::string name = raw ? raw : "?";
+      int st = 0;
+      char* dem = raw ? abi::__cxa_demangle(raw, nullptr, nullptr, &st) : nullptr;
+      if (dem && st == 0) name = dem;
+      std::free(dem);
+      size_t depth = 0, cut = std::string::npos;
+      for (size_t i = 0; i < name.size(); i++) {  // the parameter list: the last top-level '('
+        if (name[i] == '<') depth++;
+        else if (name[i] == '>' && depth) depth--;
+        else if (name[i] == '(' && depth == 0) cut = i;
+      }
+      if (cut != std::string::npos) name.resize(cut);
+      if (name.compare(0, 5, "void ") == 0) name.erase(0, 5);
+      for (size_t p; (p = name.find("prism::")) != std::string::npos;) name.erase(p, 7);
+      if (name == prev) {
+        run++;
+      } else {
+        flush();
+        prev = name;
+        run = 1;
+      }
+    }
+    flush();
+    ctx->kernels = out;
+  }
+  return ctx->kernels.c_str();
 }
 
 // Host payloads go through the pinned ring (stage_h2d); device payloads
@@ -1212,7 +1294,7 @@ static prism_hip_weight* upload_impl(prism_hip_ctx* ctx, const void* src, bool s
     if (rc == PRISM_HIP_OK) {
       const size_t pieces = prism::gi_bytes(w->gi, dm, dn, bits) / 16;
       const unsigned grid = (unsigned)std::min<size_t>((pieces + 255) / 256, 16384);
-      hipLaunchKernelGGL(prism::k_gi_pack, dim3(grid), dim3(256), 0, ctx->stream,
+      PRISM_LAUNCH(prism::k_gi_pack, dim3(grid), dim3(256), 0, ctx->stream,
                          reinterpret_cast<const uint8_t*>(s), w->d, dm, dn, w->gi, bits);
       e = hipGetLastError();
       if (e != hipSuccess) rc = fail(ctx, PRISM_HIP_ERR_DEVICE, "GI pack: %s", hipGetErrorString(e));
@@ -1277,6 +1359,7 @@ int prism_hip_gemv_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void
   if (!d_x || !d_y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
   if (batch == 0) return PRISM_HIP_OK;
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   rc = launch_gemv(ctx, w, nullptr, d_x, batch, d_y, pick_stream(ctx, stream));
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;
@@ -1289,6 +1372,7 @@ int prism_hip_gemv(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t
   if (!x || !y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
   if (batch == 0) return PRISM_HIP_OK;
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   const size_t xb = (size_t)batch * w->dim_n * 2, yb = (size_t)batch * w->dim_m * 2;
   const size_t xoff = 0, yoff = (xb + 255) & ~(size_t)255;
   if ((rc = ensure_stage(ctx, yoff + yb))) return rc;
@@ -1319,6 +1403,7 @@ int prism_hip_gateup_swiglu_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate
   if (rc) return rc;
   if (!d_x || !d_y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   rc = launch_gemv(ctx, gate, up, d_x, 1, d_y, pick_stream(ctx, stream));
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;
@@ -1331,6 +1416,7 @@ int prism_hip_gateup_swiglu(prism_hip_ctx* ctx, const prism_hip_weight* gate, co
   if (rc) return rc;
   if (!x || !y) return fail(ctx, PRISM_HIP_ERR_NULL, "x or y is NULL");
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   const size_t xb = (size_t)gate->dim_n * 2, yb = (size_t)gate->dim_m * 2;
   const size_t yoff = (xb + 255) & ~(size_t)255;
   if ((rc = ensure_stage(ctx, yoff + yb))) return rc;
@@ -1351,6 +1437,7 @@ int prism_hip_gate_up_dev(prism_hip_ctx* ctx, const prism_hip_weight* gate, cons
   if (rc) return rc;
   if (!d_x || !d_gate_out || !d_up_out) return fail(ctx, PRISM_HIP_ERR_NULL, "x or an output is NULL");
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   rc = launch_gemv(ctx, gate, up, d_x, 1, d_gate_out, pick_stream(ctx, stream), d_up_out);
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;
@@ -1363,6 +1450,7 @@ int prism_hip_gate_up(prism_hip_ctx* ctx, const prism_hip_weight* gate, const pr
   if (rc) return rc;
   if (!x || !gate_out || !up_out) return fail(ctx, PRISM_HIP_ERR_NULL, "x or an output is NULL");
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   const size_t xb = (size_t)gate->dim_n * 2, yb = (size_t)gate->dim_m * 2;
   const size_t yoff = (xb + 255) & ~(size_t)255, y2off = yoff + ((yb + 255) & ~(size_t)255);
   if ((rc = ensure_stage(ctx, y2off + yb))) return rc;
@@ -1385,6 +1473,7 @@ int prism_hip_gemm_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, const void
   if (!d_X || !d_Y) return fail(ctx, PRISM_HIP_ERR_NULL, "X or Y is NULL");
   if (M == 0) return PRISM_HIP_OK;
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   rc = launch_gemm(ctx, w, d_X, M, d_Y, pick_stream(ctx, stream));
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;
@@ -1398,6 +1487,12 @@ int prism_hip_gemm_dev_noalloc(prism_hip_ctx* ctx, const prism_hip_weight* w, co
   if (!d_X || !d_Y) return fail(ctx, PRISM_HIP_ERR_NULL, "X or Y is NULL");
   if (M == 0) return PRISM_HIP_OK;
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
+  if (!ctx->scratch) {
+    const hipError_t e = device_scratch(ctx->device, &ctx->scratch);
+    if (e != hipSuccess)
+      return fail(ctx, PRISM_HIP_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+  }
   rc = launch_gemm(ctx, w, d_X, M, d_Y, pick_stream(ctx, stream), ctx->scratch);
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;
@@ -1410,6 +1505,7 @@ int prism_hip_gemm(prism_hip_ctx* ctx, const prism_hip_weight* w, const uint16_t
   if (!X || !Y) return fail(ctx, PRISM_HIP_ERR_NULL, "X or Y is NULL");
   if (M == 0) return PRISM_HIP_OK;
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   const size_t xb = (size_t)M * w->dim_n * 2, yb = (size_t)M * w->dim_m * 2;
   const size_t yoff = (xb + 255) & ~(size_t)255;
   if ((rc = ensure_stage(ctx, yoff + yb))) return rc;
@@ -1432,6 +1528,7 @@ int prism_hip_decode_rows_dev(prism_hip_ctx* ctx, const prism_hip_weight* w, uin
   if (row0 > w->dim_m || nrows > w->dim_m - row0)
     return fail(ctx, PRISM_HIP_ERR_SHAPE, "rows [%u, %u) outside 0..%u", row0, row0 + nrows, w->dim_m);
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   rc = launch_decode(ctx, w, row0, nrows, d_out, pick_stream(ctx, stream));
   if (rc == PRISM_HIP_OK) ctx->err.clear();
   return rc;
@@ -1448,6 +1545,7 @@ int prism_hip_lut_embed(prism_hip_ctx* ctx, const prism_hip_weight* w, uint32_t 
     return PRISM_HIP_OK;
   }
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   const size_t ob = (size_t)w->dim_n * 2;
   if ((rc = ensure_stage(ctx, ob))) return rc;
   if ((rc = launch_decode(ctx, w, token, 1, ctx->d_stage, ctx->stream))) return rc;
@@ -1464,8 +1562,9 @@ int prism_hip_stream_read_dev(prism_hip_ctx* ctx, const void* d_buf, size_t byte
   if (bytes == 0) return PRISM_HIP_OK;
   if (bytes >= (1ull << 31)) return fail(ctx, PRISM_HIP_ERR_SIZE, "%zu bytes: at most 2 GiB - 1 per call", bytes);
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   const unsigned grid = (unsigned)((bytes + prism::kStreamBytesPerBlock - 1) / prism::kStreamBytesPerBlock);
-  hipLaunchKernelGGL(prism::k_stream_read, dim3(grid), dim3(64), 0, pick_stream(ctx, stream),
+  PRISM_LAUNCH(prism::k_stream_read, dim3(grid), dim3(64), 0, pick_stream(ctx, stream),
                      reinterpret_cast<const uint8_t*>(d_buf), (uint32_t)bytes, reinterpret_cast<uint32_t*>(d_sink));
   HIP_TRY(ctx, hipGetLastError());
   ctx->err.clear();
@@ -1510,7 +1609,7 @@ static int launch_palettize(prism_hip_ctx* ctx, const float* d_w, uint32_t out_d
   if (lds + stat <= ctx->lds_max) {
     for (uint32_t r0 = 0; r0 < out_dim; r0 += kMaxGrid) {
       const uint32_t rows = std::min(kMaxGrid, out_dim - r0);
-      hipLaunchKernelGGL(prism::k_palettize<true>, dim3(rows), dim3(64), lds, st, d_w, in_dim, k, max_iter, seeds,
+      PRISM_LAUNCH(prism::k_palettize<true>, dim3(rows), dim3(64), lds, st, d_w, in_dim, k, max_iter, seeds,
                          r0, nullptr, lut, idx);
       HIP_TRY(ctx, hipGetLastError());
     }
@@ -1522,7 +1621,7 @@ static int launch_palettize(prism_hip_ctx* ctx, const float* d_w, uint32_t out_d
   HIP_TRY(ctx, hipMallocAsync(&ws, wsb, st));
   for (uint32_t r0 = 0; r0 < out_dim; r0 += chunk) {
     const uint32_t rows = std::min(chunk, out_dim - r0);
-    hipLaunchKernelGGL(prism::k_palettize<false>, dim3(rows), dim3(64), 0, st, d_w, in_dim, k, max_iter, seeds,
+    PRISM_LAUNCH(prism::k_palettize<false>, dim3(rows), dim3(64), 0, st, d_w, in_dim, k, max_iter, seeds,
                        r0, reinterpret_cast<float*>(ws), lut, idx);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -1543,6 +1642,7 @@ int prism_hip_palettize(prism_hip_ctx* ctx, const float* w, uint32_t out_dim, ui
   if (out_dim == 0) return PRISM_HIP_OK;
   if (!payload || (!w && in_dim)) return fail(ctx, PRISM_HIP_ERR_NULL, "weights or payload is NULL");
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   const size_t wb = (size_t)out_dim * in_dim * 4, pb = prism_hip_palettize_bytes(out_dim, in_dim);
   const size_t poff = (wb + 255) & ~(size_t)255;
   if ((rc = ensure_stage(ctx, poff + pb))) return rc;
@@ -1566,6 +1666,7 @@ int prism_hip_palettize_dev(prism_hip_ctx* ctx, const void* d_w, uint32_t out_di
   if (out_dim == 0) return PRISM_HIP_OK;
   if (!d_payload || (!d_w && in_dim)) return fail(ctx, PRISM_HIP_ERR_NULL, "weights or payload is NULL");
   DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
   rc = launch_palettize(ctx, reinterpret_cast<const float*>(d_w), out_dim, in_dim, k, max_iter, ps,
                         reinterpret_cast<uint8_t*>(d_payload), pick_stream(ctx, stream));
   if (rc == PRISM_HIP_OK) ctx->err.clear();

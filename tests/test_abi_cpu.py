@@ -45,6 +45,7 @@ def test_null_handling_without_gpu(pe):
     assert lib.prism_hip_backend_gemv(None, b"k", None, 0, None, 0) == -1
     assert lib.prism_hip_backend_len(None) == 0
     assert lib.prism_hip_weight_upload(None, None, 0, 1, 8, 4, 0) is None
+    assert lib.prism_hip_last_kernels(None) == b""
 
 
 def test_ctx_create_reports_error_when_no_gpu(pe):

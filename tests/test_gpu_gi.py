@@ -419,3 +419,65 @@ def test_gi8_gemm(pe, oracle, gpu_ctx, M):
     for i, m in enumerate(rows):
         assert _rel(Y[m], ref[i]) <= TOL
     w.free()
+
+
+@pytest.mark.parametrize("batch,kernel", [(1, "k_gemv_lpr8<8, 1, 1, 0, 64>"), (2, "k_gemv_lpr8<8, 1, 2, 0, 64>"),
+                                          (4, "k_gemv_lpr8<8, 1, 4, 0, 64>"), (5, "k_gemv_lpr8<8, 1, 8, 0, 64>"),
+                                          (8, "k_gemv_lpr8<8, 1, 8, 0, 64>")])
+def test_gi8_gemv_k8192(pe, oracle, gpu_ctx, batch, kernel):
+    """8-bit GI with K = 8192: each wave's 64 chunks as a compile-time
+    count.  1, 2 and 4 vectors a pass, and the 8-vector form for 5..8
+    (x of five 8192-element vectors, 5 x 4100 dwords, does not fit
+    k_gemv_lpr8m's 16512-dword LDS), against the oracle; the library's
+    launch report names the kernel that ran."""
+    N, K = 14336, 8192
+    assert _gi(N, K, 8)
+    t = pe.synth_tensor(N, K, 8, seed=K + batch)
+    x = pe.synth_x(batch, K, seed=batch + 81)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi8 gemv {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    assert gpu_ctx.last_kernels() == kernel
+    _check(y, oracle.gemv(x, t.payload, N, K, 8, threads=8), f"GI8 {N}x{K} batch {batch}")
+    w.free()
+
+
+def test_gi8_gate_up_k8192(pe, oracle, gpu_ctx):
+    """8-bit GI gate/up at K = 8192 (k_gemv_lpr8 with two matrices and 64
+    chunks per wave): the SwiGLU form against the oracle, the two-output
+    form bit for bit against the separate GEMVs."""
+    N, K = 14336, 8192
+    tg = pe.synth_tensor(N, K, 8, seed=K + 21)
+    tu = pe.synth_tensor(N, K, 8, seed=K + 22)
+    x = pe.synth_x(1, K, seed=K + 23)
+    wg, wu = gpu_ctx.upload_tensor(tg), gpu_ctx.upload_tensor(tu)
+    print(f"gi8 gate_up {N}x{K}", flush=True)
+    y = gpu_ctx.gateup_swiglu(wg, wu, x)
+    assert gpu_ctx.last_kernels() == "k_gemv_lpr8<8, 2, 1, 1, 64>"
+    _check(y, oracle.gateup_swiglu(x[0], tg.payload, tu.payload, N, K, 8, threads=8), "GI8 K=8192 SwiGLU")
+    yg, yu = gpu_ctx.gate_up(wg, wu, x)
+    assert gpu_ctx.last_kernels() == "k_gemv_lpr8<8, 2, 1, 2, 64>"
+    assert np.array_equal(yg, gpu_ctx.gemv(wg, x)[0])
+    assert np.array_equal(yu, gpu_ctx.gemv(wu, x)[0])
+    _check(yg, oracle.gemv(x, tg.payload, N, K, 8, threads=8), "GI8 K=8192 gate")
+    wg.free()
+    wu.free()
+
+
+def test_last_kernels_reports_the_dispatch(pe, gpu_ctx):
+    """prism_hip_last_kernels names the hero's lane-per-row kernel, repeats
+    as " x n" for passes, and is cleared by the next call."""
+    N, K = 14336, 4096
+    t = pe.synth_tensor(N, K, 4, seed=5)
+    w = gpu_ctx.upload_tensor(t)
+    gpu_ctx.gemv(w, pe.synth_x(1, K, seed=1))
+    assert gpu_ctx.last_kernels() == "k_gemv_lpr<8, 1, 1, 0, 16>"
+    gpu_ctx.gemv(w, pe.synth_x(2, K, seed=1))
+    assert gpu_ctx.last_kernels() == "k_gemv_lpr<8, 1, 2, 0, 16>"
+    gpu_ctx.gemv(w, pe.synth_x(40, K, seed=1))  # 16 + 16 + 8 vectors on the matrix cores
+    assert gpu_ctx.last_kernels() == "k_gemv_mfma<4, true> x3"
+    small = gpu_ctx.upload_tensor(pe.synth_tensor(4864, 896, 4, seed=6))
+    gpu_ctx.gemv(small, pe.synth_x(1, 896, seed=1))
+    assert gpu_ctx.last_kernels().startswith("k_gemv_tile<")
+    w.free()
+    small.free()

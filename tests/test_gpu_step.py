@@ -242,3 +242,42 @@ def test_step_depth_sweep(gpu_ctx):
     # no jump: each doubling of depth at most triples the error
     for a, b in zip(depths, depths[1:]):
         assert errs[b] <= 3.0 * max(errs[a], 1e-4), f"{a} -> {b} layers: {errs[a]:.3e} -> {errs[b]:.3e}"
+
+
+def test_step_every_layer_alone_at_2e3(gpu_ctx):
+    """Each of config 3's 24 layers on its own, at the single-GEMV bound.
+    Layer l of the Qwen2.5-0.5B weights (seed 1003), with its own 512
+    cached tokens, runs as a one-layer model under the 151936 x 896 tied LM
+    head, one step at pos 512, and its logits must lie within 2e-3 of the
+    sequential oracle's: no layer may hide a defect inside the depth
+    sweep's drift bound."""
+    cfg = pe.Qwen2Config()
+    one = pe.Qwen2Config(n_layers=1)
+    embed, layers = pe.synth_weights(cfg, 1003)
+    emb_p, lay_p = pe.model.payloads(embed, layers)
+    kvs = pe.synth_kv(cfg, 512, 1003)
+    w_emb = gpu_ctx.upload_tensor(embed)
+    errs = []
+    try:
+        for l in range(cfg.n_layers):
+            print(f"layer {l} alone", flush=True)
+            m = pe.Model(gpu_ctx, one, max_seq=600)
+            m.set_embedding(w_emb)
+            ws = [gpu_ctx.upload_tensor(t) for t in layers[l]]
+            m.set_layer(0, ws)
+            for w in ws:
+                w.free()
+            k, v = kvs[l]
+            m.kv_append(0, k, v)
+            got = m.step(42, 512)
+            m.close()
+            kv = oracle.KVState(1, cfg.kv_dim, 513)
+            for t in range(512):
+                kv.append(0, k[t], v[t])
+            want = oracle.decode_step(one.oracle_dims(), one.rms_eps, emb_p, [lay_p[l]], kv, 42, 512, threads=16)
+            errs.append(pe.rel_err(got, want))
+            print(f"  layer {l:2d}: logits rel err {errs[-1]:.3e}", flush=True)
+    finally:
+        w_emb.free()
+    worst = int(np.argmax(errs))
+    assert max(errs) <= STEP_TOL, f"layer {worst}: {errs[worst]:.3e}"

@@ -198,3 +198,19 @@ def test_oracle_threads_bit_identical(pe, oracle):
     x = pe.synth_x(1, 512, seed=9)[0]
     assert np.array_equal(oracle.lut_gemv4(x, t.payload, 300, 512),
                           oracle.lut_gemv4(x, t.payload, 300, 512, threads=4))
+
+
+def test_rel_err_reads_fp16_values_not_bit_patterns(pe):
+    """The per-vector bound is taken on fp16 values: a 5 % error on the
+    largest output is 5e-2 there, though the same vectors compared as
+    integer bit patterns differ by under 2e-3 (the metric a GPU test once
+    used by mistake)."""
+    rng = np.random.default_rng(0)
+    ref = (rng.standard_normal(4096) * 0.3).astype(np.float16)
+    i = int(np.argmax(np.abs(ref)))
+    bad = ref.copy()
+    bad[i] = np.float16(float(ref[i]) * 1.05)
+    as_ints = float(np.abs(bad.view(np.uint16).astype(np.float32) - ref.view(np.uint16).astype(np.float32)).max()
+                    / np.abs(ref.view(np.uint16).astype(np.float32)).max())
+    assert as_ints < 2e-3
+    assert pe.rel_err(bad.view(np.uint16), ref.view(np.uint16)) > 4e-2

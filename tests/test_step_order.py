@@ -76,3 +76,24 @@ def test_decode_step_order_drift_grows_with_depth():
     assert e1 <= 2e-3          # one layer: within the per-vector GEMV bound
     assert e1 < e4 < e24       # grows with depth
     assert 2e-3 < e24 < 1e-2   # 24 layers: past 2e-3 with nothing but the order changed
+
+
+def test_fold_mode_refuses_sums_past_its_block_capacity():
+    """Mode 1 keeps at most 2048 block sums (131072 terms).  A decode step
+    whose attention runs over more positions than that would need more: the
+    oracle raises instead of dropping the terms past the limit, and mode 0
+    (the reference's fold) has no such limit."""
+    cfg = pe.Qwen2Config(n_layers=1, hidden=64, n_heads=1, n_kv_heads=1, head_dim=64, intermediate=64,
+                         vocab=32)
+    embed, layers = pe.synth_weights(cfg, 3)
+    emb_p, lay_p = pe.model.payloads(embed, layers)
+    n = 2048 * 64 + 1  # softmax and value sums over n + 1 positions
+    kv = oracle.KVState(1, cfg.kv_dim, n + 1)
+    blk = oracle.kv_quant(np.zeros(cfg.kv_dim, np.uint16))
+    ts = cfg.kv_dim + 4
+    kv.k[0][:n * ts] = np.tile(blk, n)
+    kv.v[0][:n * ts] = np.tile(blk, n)
+    kv.len[0] = n
+    with pytest.raises(ValueError, match="131072"):
+        oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv.copy(), 1, n, fold=1)
+    oracle.decode_step(cfg.oracle_dims(), cfg.rms_eps, emb_p, lay_p, kv, 1, n, fold=0)

@@ -60,3 +60,42 @@ def test_gemm_noalloc_errors(pe, gpu_ctx):
     gpu_ctx.gemm_dev_noalloc(w, dX, 0, dX)
     torch.cuda.synchronize()
     w.free()
+
+
+def test_gemm_noalloc_replayed_from_a_hip_graph(pe, gpu_ctx):
+    """The no-alloc GEMM captured in a HIP graph: the split-K path (4-bit
+    14336 x 4096, M = 64: k_gemm_w4 in 4 K splits writing the static
+    scratch, then k_gemm_split_sum) makes no call that capture rejects, and
+    every replay, each with new X copied in eagerly between replays,
+    equals prism_hip_gemm_dev on the same X bit for bit."""
+    import torch
+    N, K, M = 14336, 4096, 64
+    t = pe.synth_tensor(N, K, 4, seed=404)
+    w = gpu_ctx.upload_tensor(t)
+    s = torch.cuda.Stream()
+    dX = torch.from_numpy(pe.synth_x(M, K, seed=1).view(np.int16)).cuda()
+    dY = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    want = torch.zeros_like(dY)
+    torch.cuda.synchronize()
+    print("[no_alloc graph] eager call", flush=True)
+    gpu_ctx.gemm_dev_noalloc(w, dX, M, dY, s)  # first call looks up the scratch address
+    s.synchronize()
+    assert "k_gemm_split_sum" in gpu_ctx.last_kernels()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        gpu_ctx.gemm_dev_noalloc(w, dX, M, dY, s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        print(f"[no_alloc graph] replay {i}", flush=True)
+        dX.copy_(torch.from_numpy(pe.synth_x(M, K, seed=10 + i).view(np.int16)))
+        dY.fill_(-1)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            g.replay()
+        s.synchronize()
+        gpu_ctx.gemm_dev(w, dX, M, want, s)
+        s.synchronize()
+        a, b = want.cpu().numpy(), dY.cpu().numpy()
+        assert np.array_equal(a, b), f"replay {i}: {int(np.sum(a != b))} of {a.size} outputs differ"
+    del g
+    w.free()
