@@ -108,7 +108,8 @@ def test_model_config_fields_match():
     assert cfields == rfields
 
 
-@pytest.mark.parametrize("path", [RUST, os.path.join(ROOT, "integration", "rust", "src", "backend", "hip.rs")])
+@pytest.mark.parametrize("path", [RUST, os.path.join(ROOT, "integration", "rust", "src", "backend", "hip.rs"),
+                                  os.path.join(ROOT, "integration", "rust", "src", "lut", "plan_hip.rs")])
 def test_integration_md_shows_the_files(path):
     md = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     blocks = re.findall(r"```rust\n(.*?)```", md, re.S)
