@@ -5,9 +5,13 @@ Default workload (BASELINE.json metric): 4-bit palettized GEMV at batch 1,
 K=4096, N=14336 ("hero").  A step is one GEMV over one weight matrix with
 the activations already in HBM.  Steps rotate over enough distinct device
 copies of the weights (>= 2 x the 256 MB Infinity Cache) that every step
-reads its weights from HBM.  The K timed steps are captured once into a HIP
-graph and replayed, so the timed region holds K back-to-back kernels and no
-host launch cost.
+reads its weights from HBM.  The timed region holds exactly K back-to-back
+kernels and no host launch cost: a bounded device-side spin runs while the
+host enqueues them (up to 200 steps eagerly, right after the warm-up
+launches; more steps captured once into a HIP graph and replayed), and
+events on the launch stream bracket the K launches.  In the same process the
+library's streaming-read kernel is timed the same way over as many bytes per
+launch ("floor": the kernel's ratio to a pure read of its bytes).
 
 value = effective weight bytes (index + LUT bytes) x K / timed seconds.
 
@@ -133,42 +137,60 @@ def device_busy(stream, ms: float = 2.0) -> None:
 _SPIN_CYCLES_PER_MS = None
 
 
+# Up to this many timed steps the launches are issued eagerly (the spin ahead
+# of them covers the host's enqueue of every launch); beyond it they are
+# replayed from one HIP graph, whose fixed cost per replay (about 11 us on
+# MI355X, inside any event window around the replay) a short run cannot
+# amortise.  MI355X, hero: eager 20 steps 6.57-6.60 us per launch, graph 20
+# steps 6.93-6.97, graph 2000 steps 6.39-6.41 (kernel-argument preloading on).
+EAGER_MAX_STEPS = 200
+
+
 def time_launches(launch, steps: int, warmup: int, stream, use_graph: bool):
-    """Warm up, then time exactly `steps` launches (captured into one HIP
-    graph and replayed, or issued eagerly) with events on `stream`, behind a
-    device-side spin (device_busy).  Returns (device ms, wall ms)."""
+    """Time exactly `steps` launches with events on `stream`, behind a
+    device-side spin (device_busy) so that the window holds device work only.
+    Up to EAGER_MAX_STEPS (or without use_graph) the `warmup` launches go
+    eagerly right before the timed ones, with no synchronisation between
+    them, so the first timed launch follows the same kernel; above it the
+    steps are captured once into a HIP graph and the timed replay follows an
+    untimed one.  Returns (device ms, wall ms, launch mode)."""
     import torch
     with torch.cuda.stream(stream):
         for i in range(warmup):
             launch(i)
     torch.cuda.synchronize()
     graph = None
-    if use_graph:
+    if use_graph and steps > EAGER_MAX_STEPS:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             for i in range(steps):
                 launch(i)
         torch.cuda.synchronize()
-        with torch.cuda.stream(stream):
-            graph.replay()  # untimed first replay (graph upload)
-        torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
-    device_busy(stream)
     with torch.cuda.stream(stream):
-        e0.record(stream)
         if graph is not None:
+            device_busy(stream)
+            graph.replay()  # untimed replay right before the timed one
+            e0.record(stream)
             graph.replay()
+            e1.record(stream)
         else:
+            # the host enqueues every launch while the GPU spins (Python
+            # issues a launch in about 12 us)
+            device_busy(stream, max(2.0, 0.03 * (warmup + steps)))
+            for i in range(warmup):
+                launch(i)
+            e0.record(stream)
             for i in range(steps):
                 launch(i)
-        e1.record(stream)
+            e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     del graph
-    return e0.elapsed_time(e1), wall * 1e3
+    return e0.elapsed_time(e1), wall * 1e3, ("hip_graph" if use_graph and steps > EAGER_MAX_STEPS else "eager")
 
 
 def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
@@ -628,9 +650,8 @@ def main() -> int:
     kernel_name = ctx.last_kernels()
     log(f"[bench] kernels of one step: {kernel_name}")
 
-    ms, wall_ms = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph)
+    ms, wall_ms, launch_mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph)
     ms_step = ms / args.steps
-    launch_mode = "eager" if args.no_graph else "hip_graph"
     log(f"[bench] timed {args.steps} steps ({launch_mode}, behind a device-side spin): {ms:.3f} ms on device "
         f"events, {wall_ms:.3f} ms wall")
 
@@ -644,7 +665,7 @@ def main() -> int:
 
         def flaunch(i: int) -> None:
             ctx.stream_read_dev(fbufs[i % copies], wb, fsink, stream)
-        fms, _ = time_launches(flaunch, args.steps, args.warmup, stream, not args.no_graph)
+        fms, _, _ = time_launches(flaunch, args.steps, args.warmup, stream, not args.no_graph)
         f_us = fms / args.steps * 1e3
         floor = {"kernel": "k_stream_read", "us_per_launch": round(f_us, 4),
                  "GBps": round(wb / (f_us * 1e-6) / 1e9, 2), "kernel_over_floor": round(ms_step * 1e3 / f_us, 4),

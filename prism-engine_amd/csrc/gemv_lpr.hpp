@@ -85,7 +85,7 @@ constexpr int kLprAhead = 5;
 constexpr int kLprXBlock = 2;
 
 template <int S, int NM, int NB, int EPI, int NCH = 0>
-__global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
+__device__ __forceinline__ void lpr_body(const LprArgs& a) {
   static_assert(S == 4 || S == 8 || S == 16, "waves per group");
   static_assert(NM == 1 || NM == 2, "one matrix or gate + up");
   static_assert(NB == 1 || NB == 2, "batch vectors per pass");
@@ -274,6 +274,13 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(LprArgs a) {
   }
 }
 
+template <int S, int NM, int NB, int EPI, int NCH = 0>
+__global__ __launch_bounds__(64 * S) void k_gemv_lpr(const uint8_t* w, const uint8_t* w2, const uint16_t* x,
+                                                     uint16_t* y, uint16_t* y2, uint32_t N, uint32_t K,
+                                                     uint32_t nb, uint32_t G) {
+  lpr_body<S, NM, NB, EPI, NCH>(lpr_args(w, w2, x, y, y2, N, K, nb, G));
+}
+
 // Chunk loads of k_gemv_lpr8 when the wave's chunk count is a compile-time
 // constant: first / ahead as for k_gemv_lpr.  cfg4 shape (14336 x 4096,
 // 8-bit, 56-row groups), MI355X, timing copies: (5, 5) with 2-chunk x
@@ -300,7 +307,7 @@ constexpr int kLpr8Ahead = 5;
 //    multiples of 4).
 // Requires K % 512 == 0, 16-byte aligned x and the weight block below 2 GiB.
 template <int S, int NM, int NB, int EPI, int NCH = 0>
-__global__ __launch_bounds__(64 * S) void k_gemv_lpr8(LprArgs a) {
+__device__ __forceinline__ void lpr8_body(const LprArgs& a) {
   static_assert(S == 8, "eight waves: 32 table entries each");
   static_assert(NM == 1 || NM == 2, "one matrix or gate + up");
   static_assert(NB == 1 || NB == 2 || NB == 4 || NB == 8, "batch vectors per pass");
@@ -451,6 +458,13 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr8(LprArgs a) {
         a.y[(size_t)b * N + row] = f2h(s[0]);
     }
   }
+}
+
+template <int S, int NM, int NB, int EPI, int NCH = 0>
+__global__ __launch_bounds__(64 * S) void k_gemv_lpr8(const uint8_t* w, const uint8_t* w2, const uint16_t* x,
+                                                      uint16_t* y, uint16_t* y2, uint32_t N, uint32_t K,
+                                                      uint32_t nb, uint32_t G) {
+  lpr8_body<S, NM, NB, EPI, NCH>(lpr_args(w, w2, x, y, y2, N, K, nb, G));
 }
 
 // k_gemv_lpr8m, the 8-bit GEMV of 5..8 vectors with these lookups feeding

@@ -49,7 +49,7 @@ namespace prism {
 // 12.1 / 13.5-13.6 / 13.5-13.8, so up to 4 stay with k_gemv_lpr8.  With x
 // read from global memory per MFMA 17.7 / 18.1 us at 4 / 8; 2 or 8 double
 // steps ahead, or two accumulators, no faster.
-__global__ __launch_bounds__(512) void k_gemv_lpr8m(LprArgs a) {
+__device__ __forceinline__ void lpr8m_body(const LprArgs& a) {
   constexpr int Q = 4;  // K quarters
   constexpr int AH = kLpr8mAhead;
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -180,9 +180,15 @@ __global__ __launch_bounds__(512) void k_gemv_lpr8m(LprArgs a) {
   }
 }
 
+__global__ __launch_bounds__(512) void k_gemv_lpr8m(const uint8_t* w, const uint8_t* w2, const uint16_t* x,
+                                                     uint16_t* y, uint16_t* y2, uint32_t N, uint32_t K, uint32_t nb,
+                                                     uint32_t G) {
+  lpr8m_body(lpr_args(w, w2, x, y, y2, N, K, nb, G));
+}
+
 hipError_t launch_gemv_lpr8m(dim3 groups, hipStream_t st, const LprArgs& a) {
   note_launch(reinterpret_cast<const void*>(&k_gemv_lpr8m));
-  hipLaunchKernelGGL(k_gemv_lpr8m, groups, dim3(512), 0, st, a);
+  hipLaunchKernelGGL(k_gemv_lpr8m, groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
   return hipGetLastError();
 }
 

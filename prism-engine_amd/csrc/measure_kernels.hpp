@@ -18,8 +18,8 @@ namespace prism {
 constexpr int kStreamLoads = 16;                       // 16-byte loads per lane
 constexpr uint32_t kStreamBytesPerBlock = 64 * 16 * kStreamLoads;  // 16 KB
 
-__global__ __launch_bounds__(64) void k_stream_read(const uint8_t* __restrict__ p, uint32_t bytes,
-                                                    uint32_t* __restrict__ sink) {
+__device__ __forceinline__ void stream_read_body(const uint8_t* __restrict__ p, uint32_t bytes,
+                                                 uint32_t* __restrict__ sink) {
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
   // every offset is in the VGPR offset: past `bytes` the range check returns zeros
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)bytes, 0x00020000);
@@ -31,6 +31,11 @@ __global__ __launch_bounds__(64) void k_stream_read(const uint8_t* __restrict__ 
 #pragma unroll
   for (int u = 0; u < kStreamLoads; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   if (acc == 0x9E3779B9u) sink[blockIdx.x & 255u] = acc;
+}
+
+__global__ __launch_bounds__(64) void k_stream_read(const uint8_t* __restrict__ p, uint32_t bytes,
+                                                    uint32_t* __restrict__ sink) {
+  stream_read_body(p, bytes, sink);
 }
 
 }  // namespace prism

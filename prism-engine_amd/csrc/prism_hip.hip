@@ -718,11 +718,11 @@ void launch_lpr(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
   const uint32_t NC = a.K / 32;
   const uint32_t nch = NC % S == 0 ? NC / S : 0;
   if (nch == 16)
-    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI, 16>), groups, dim3(64 * S), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI, 16>), groups, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
   else if (nch == 8)
-    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI, 8>), groups, dim3(64 * S), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI, 8>), groups, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
   else
-    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI>), groups, dim3(64 * S), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI>), groups, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
 }
 
 // 8-bit GI weights: k_gemv_lpr8 with the wave's chunk count as a
@@ -739,13 +739,13 @@ template <int NM, int NB, int EPI>
 int launch_lpr8(prism_hip_ctx* ctx, dim3 groups, hipStream_t st, const prism::LprArgs& a) {
   const uint32_t nch = a.K / 16 / 8;
   if (nch == 32)
-    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 32>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 32>), groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
   else if (nch == 16)
-    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 16>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 16>), groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
   else if (nch == 64)
-    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 64>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI, 64>), groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
   else if constexpr (NB < 8)
-    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI>), groups, dim3(512), 0, st, a);
+    PRISM_LAUNCH((prism::k_gemv_lpr8<8, NM, NB, EPI>), groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
   else
     return fail(ctx, PRISM_HIP_ERR_SHAPE, "k_gemv_lpr8: %d vectors need a compile-time chunk count (K = %u)", NB,
                 a.K);
