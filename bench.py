@@ -136,26 +136,93 @@ def device_busy(stream, ms: float = 2.0) -> None:
 
 _SPIN_CYCLES_PER_MS = None
 
+# HIP event flags (hip_runtime_api.h).  The timed region is bracketed by
+# events created with hipEventDisableSystemFence, which HIP documents for
+# timing: recording such an event does not write back and invalidate the
+# caches at system scope, a cost (and a disturbance of the next kernel) that
+# an event window of a few launches would otherwise carry at both edges.
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000
+HIP_EVENT_RELEASE_TO_DEVICE = 0x40000000
+TIMING_EVENT_FLAGS = HIP_EVENT_DISABLE_SYSTEM_FENCE
+
+
+class HipEvent:
+    """A timing event of the HIP runtime (the library torch already loaded),
+    created with explicit flags; record() on a torch stream."""
+    _hip = None
+
+    def __init__(self, flags: int = TIMING_EVENT_FLAGS):
+        import ctypes
+        if HipEvent._hip is None:
+            # the HIP runtime this process already runs on (torch's copy, which
+            # libprism_hip.so binds to by soname); loading another copy by name
+            # would start a second runtime
+            with open("/proc/self/maps") as f:
+                paths = sorted({ln.split()[-1] for ln in f if "libamdhip64" in ln and "/" in ln})
+            if not paths:
+                raise RuntimeError("no HIP runtime loaded in this process")
+            hip = ctypes.CDLL(paths[0])
+            hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+            hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            HipEvent._hip = hip
+        self.h = ctypes.c_void_p()
+        self._check(HipEvent._hip.hipEventCreateWithFlags(ctypes.byref(self.h), flags), "hipEventCreateWithFlags")
+
+    @staticmethod
+    def _check(rc: int, what: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: hipError {rc}")
+
+    def record(self, stream) -> None:
+        self._check(HipEvent._hip.hipEventRecord(self.h, stream.cuda_stream), "hipEventRecord")
+
+    def elapsed_time(self, end: "HipEvent") -> float:
+        import ctypes
+        self._check(HipEvent._hip.hipEventSynchronize(end.h), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self._check(HipEvent._hip.hipEventElapsedTime(ctypes.byref(ms), self.h, end.h), "hipEventElapsedTime")
+        return ms.value
+
+    def __del__(self):
+        if HipEvent._hip is not None and self.h:
+            HipEvent._hip.hipEventDestroy(self.h)
+
 
 # Up to this many timed steps the launches are issued eagerly (the spin ahead
 # of them covers the host's enqueue of every launch); beyond it they are
 # replayed from one HIP graph, whose fixed cost per replay (about 11 us on
 # MI355X, inside any event window around the replay) a short run cannot
-# amortise.  MI355X, hero: eager 20 steps 6.57-6.60 us per launch, graph 20
-# steps 6.93-6.97, graph 2000 steps 6.39-6.41 (kernel-argument preloading on).
+# amortise.  MI355X, hero, one box: eager 20 steps 6.63-6.73 us per launch,
+# graph 2000 steps 6.44 (a graph replay of 20 steps: 6.93-7.0).
 EAGER_MAX_STEPS = 200
 
 
-def time_launches(launch, steps: int, warmup: int, stream, use_graph: bool):
+def time_launches(launch, steps: int, warmup: int, stream, use_graph: bool, copies: int = 1,
+                  event_flags: int = TIMING_EVENT_FLAGS):
     """Time exactly `steps` launches with events on `stream`, behind a
     device-side spin (device_busy) so that the window holds device work only.
-    Up to EAGER_MAX_STEPS (or without use_graph) the `warmup` launches go
-    eagerly right before the timed ones, with no synchronisation between
-    them, so the first timed launch follows the same kernel; above it the
-    steps are captured once into a HIP graph and the timed replay follows an
-    untimed one.  Returns (device ms, wall ms, launch mode)."""
+
+    launch(i) works on rotated input copy i % copies.  First one untimed
+    launch per copy, so that the timed launches find every copy's address
+    translations warm, as in the steady state of a long run (MI355X, hero, 20
+    eager steps: 7.36-7.55 us per launch when 15 of the 20 copies were last
+    touched at upload, 6.65-6.68 once each has been read).  Then the `warmup`
+    launches (indices 0..warmup-1) and the timed ones, which continue the
+    rotation (indices warmup..warmup+steps-1), so no timed launch reads a copy
+    read within the last few launches (still in the 256 MB MALL).
+
+    Up to EAGER_MAX_STEPS (or without use_graph) the warm-up and the timed
+    launches go eagerly one after the other with no synchronisation between
+    them; above it the timed launches are captured once into a HIP graph and
+    the timed replay follows an untimed one.  That whole sequence runs once
+    untimed, then once timed.  Returns (device ms, wall ms, launch mode)."""
     import torch
     with torch.cuda.stream(stream):
+        for i in range(copies):
+            launch(i)
         for i in range(warmup):
             launch(i)
     torch.cuda.synchronize()
@@ -164,29 +231,37 @@ def time_launches(launch, steps: int, warmup: int, stream, use_graph: bool):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             for i in range(steps):
-                launch(i)
+                launch(warmup + i)
         torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    e0 = HipEvent(event_flags)
+    e1 = HipEvent(event_flags)
+
+    def sequence() -> None:
+        with torch.cuda.stream(stream):
+            if graph is not None:
+                device_busy(stream)
+                graph.replay()  # untimed replay right before the timed one
+                e0.record(stream)
+                graph.replay()
+                e1.record(stream)
+            else:
+                # the host enqueues every launch while the GPU spins (Python
+                # issues a launch in 5-12 us); 10 ms also brings the GPU's
+                # clocks back up after the idle of the parity check
+                device_busy(stream, max(10.0, 0.03 * (warmup + steps)))
+                for i in range(warmup):
+                    launch(i)
+                e0.record(stream)
+                for i in range(steps):
+                    launch(warmup + i)
+                e1.record(stream)
+
+    # the whole sequence once untimed: the first one in a process reads
+    # 4-5 % slower (MI355X, hero, 20 steps: 6.87-6.90 against 6.58-6.65 us)
+    sequence()
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
-    with torch.cuda.stream(stream):
-        if graph is not None:
-            device_busy(stream)
-            graph.replay()  # untimed replay right before the timed one
-            e0.record(stream)
-            graph.replay()
-            e1.record(stream)
-        else:
-            # the host enqueues every launch while the GPU spins (Python
-            # issues a launch in about 12 us)
-            device_busy(stream, max(2.0, 0.03 * (warmup + steps)))
-            for i in range(warmup):
-                launch(i)
-            e0.record(stream)
-            for i in range(steps):
-                launch(i)
-            e1.record(stream)
+    sequence()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_wall
     del graph
@@ -285,8 +360,8 @@ def run_decode(args, pe, seed) -> int:
         step(i)
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done")
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    e0 = HipEvent()
+    e1 = HipEvent()
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
     device_busy(stream)
@@ -372,8 +447,8 @@ def run_palettize(args, pe, seed) -> int:
         step()
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done")
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    e0 = HipEvent()
+    e1 = HipEvent()
     t_wall = time.perf_counter()
     e0.record(stream)
     for _ in range(args.steps):
@@ -650,7 +725,7 @@ def main() -> int:
     kernel_name = ctx.last_kernels()
     log(f"[bench] kernels of one step: {kernel_name}")
 
-    ms, wall_ms, launch_mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph)
+    ms, wall_ms, launch_mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph, copies)
     ms_step = ms / args.steps
     log(f"[bench] timed {args.steps} steps ({launch_mode}, behind a device-side spin): {ms:.3f} ms on device "
         f"events, {wall_ms:.3f} ms wall")
@@ -665,7 +740,7 @@ def main() -> int:
 
         def flaunch(i: int) -> None:
             ctx.stream_read_dev(fbufs[i % copies], wb, fsink, stream)
-        fms, _, _ = time_launches(flaunch, args.steps, args.warmup, stream, not args.no_graph)
+        fms, _, _ = time_launches(flaunch, args.steps, args.warmup, stream, not args.no_graph, copies)
         f_us = fms / args.steps * 1e3
         floor = {"kernel": "k_stream_read", "us_per_launch": round(f_us, 4),
                  "GBps": round(wb / (f_us * 1e-6) / 1e9, 2), "kernel_over_floor": round(ms_step * 1e3 / f_us, 4),
