@@ -301,6 +301,36 @@ def test_gi8_gemv(pe, oracle, gpu_ctx, N, K, batch):
     w.free()
 
 
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (8192, 2112)])
+def test_gi4_decode_bit_exact_through_lpr(pe, gpu_ctx, N, K):
+    """One-hot x through the 4-bit lane-per-row GEMV (one vector): every
+    output is LUT_r[idx(r, k)] exactly.  k runs over every element of the
+    first wave's K slice (every chunk and product position; with 16 / 8
+    chunks per wave the kernel's chunk sequence is compile-time) and the
+    last 64 elements of the row (the last wave's last products, summed right
+    after the chunk sequence); 2112 (66 chunks, not a multiple of 8 waves)
+    takes the run-time loop."""
+    assert _gi(N, K)
+    t = pe.synth_tensor(N, K, 4, seed=K + 29)
+    lut, idx = pe.unpack_payload(t.payload, N, K, 4)
+    nc = K // 32
+    first = 32 * ((nc + 7) // 8)
+    ks = list(range(first)) + list(range(K - 64, K))
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi4 one-hot {N}x{K}: {len(ks)} columns", flush=True)
+    x = np.zeros((1, K), dtype=np.float16)
+    rows = np.arange(N)
+    for k in ks:
+        x[0, :] = 0
+        x[0, k] = 1.0
+        y = gpu_ctx.gemv(w, x.view(np.uint16))[0]
+        want = lut[rows, idx[:, k]]
+        want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
+        bad = np.nonzero(y != want)[0]
+        assert bad.size == 0, f"column {k}: {bad.size} rows differ (first {bad[:4]})"
+    w.free()
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (8192, 2560)])
 def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     """One-hot x: every output is LUT_r[idx(r, k)] exactly, through the
