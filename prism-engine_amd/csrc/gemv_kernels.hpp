@@ -37,9 +37,13 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 
 // Output store at device scope (global_store_short sc1: written through to
 // where every XCD reads it, so the end-of-kernel L2 writeback finds nothing
-// of it dirty).  MI355X, hero GEMV, three alternating rounds on one box:
-// 6.41-6.43 us against 6.45-6.46 with ordinary stores (system scope, sc0
-// sc1: 6.41-6.42; sc0 alone: no change; nontemporal stores were slower).
+// of it dirty).  MI355X, 4-bit hero GEMV, three alternating rounds on one
+// box: 6.41-6.43 us against 6.45-6.46 with ordinary stores (system scope,
+// sc0 sc1: 6.41-6.42; sc0 alone: no change; nontemporal stores were
+// slower).  Only the 4-bit lane-per-row GEMVs use it: in the tile GEMV the
+// decode step took 576 against 529 us per token and 4864 x 896 3.38 against
+// 3.06 us, and the 8-bit lane-per-row GEMV at 4 vectors 14.1-14.4 against
+// 14.0-14.2.
 __device__ __forceinline__ void store_out(uint16_t* p, uint16_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -450,12 +450,12 @@ __device__ __forceinline__ void lpr8_body(const LprArgs& a) {
     }
     if (live && row < N && b < a.nb) {
       if constexpr (EPI == kLprSwiglu)
-        store_out(a.y + row, swiglu_h(s[0], s[1]));
+        a.y[row] = swiglu_h(s[0], s[1]);
       else if constexpr (EPI == kLprPair) {
-        store_out(a.y + row, f2h(s[0]));
-        store_out(a.y2 + row, f2h(s[1]));
+        a.y[row] = f2h(s[0]);
+        a.y2[row] = f2h(s[1]);
       } else
-        store_out(a.y + (size_t)b * N + row, f2h(s[0]));
+        a.y[(size_t)b * N + row] = f2h(s[0]);
     }
   }
 }
