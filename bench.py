@@ -27,7 +27,9 @@ k=16, max_iter=50 as compile_to_cimage uses: fp32 params/s), floor (the
 read floor the GEMVs are held to: one launch of the library's streaming-read
 kernel over as many bytes as the hero GEMV reads, rotated the same way;
 floor8 the same over config 4's 66 MB), load (a step is one load_cimage of a Qwen2.5-0.5B-sized 4-bit .cimage: mmap,
-every tensor through the pinned staging ring, one wait; GB/s of payload).
+every tensor through the pinned staging ring, one wait; GB/s of payload), launch (an empty kernel launched back to
+back: the cost of one dependent launch, us), mfma (register-only matrix-core work on every CU and on three quarters
+of them: TFLOP/s and the rate per CU).
 """
 from __future__ import annotations
 
@@ -70,6 +72,9 @@ WORKLOADS = {
     "floor8": ("floor", 8, 14336, 4096, 1),
     # .cimage -> device: load_cimage of a Qwen2.5-0.5B-sized file
     "load": ("load", 4, 0, 0, 1),
+    # measuring sticks: one dependent launch, the matrix cores' rate
+    "launch": ("launch", 0, 0, 0, 1),
+    "mfma": ("mfma", 0, 0, 0, 1),
 }
 PCIE_PEAK_GBS = 63.0  # PCIe 5.0 x16, one direction
 DECODE_KV_LEN = 512
@@ -616,6 +621,62 @@ def run_load(args, pe, seed) -> int:
     return 0
 
 
+def run_probe(args, pe, kind: str) -> int:
+    """The two measuring sticks behind claims about the chains of small
+    kernels and about the GEMM (measure_kernels.hpp; no counterpart in the
+    reference).  launch: one empty one-wave kernel per step, launched back
+    to back like the decode step's dependent kernels (value: us per launch).
+    mfma: register-only matrix-core work, every CU (num_cu workgroups of one
+    wave per SIMD) and three quarters of them, timed the same way as the
+    GEMV workloads (value: TFLOP/s over all CUs; the line also carries the
+    rate per CU at 3/4 of them)."""
+    import torch
+    ctx = pe.Context(0)
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.Stream(device=dev)
+    ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    if kind == "launch":
+        def launch(i: int) -> None:
+            ctx.launch_empty_dev(stream)
+        ms, wall_ms, mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph)
+        us = ms / args.steps * 1e3
+        log(f"[bench] empty kernel, {args.steps} launches ({mode}): {us:.3f} us per launch")
+        rec = {"metric": "dependent launch us (empty one-wave kernel, back to back)", "value": round(us, 4),
+               "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "ms_per_step": round(ms / args.steps, 6), "higher_is_better": False, "scaling": "weak",
+               "vs_baseline": None, "dtype": "none", "data": "none",
+               "config": {"workload": "launch", "kind": "probe", "launch": mode},
+               "roofline": None, "cpu_baseline": None}
+        print(json.dumps(rec), flush=True)
+        return 0
+    sink = torch.zeros(256, dtype=torch.float32, device=dev)
+    iters = 512
+    flop_per_group = 4 * iters * 16 * 2 * 32 * 32 * 16
+    out = {}
+    for groups in (ncu, (3 * ncu) // 4):
+        def launch(i: int, g=groups) -> None:
+            ctx.mfma_probe_dev(g, iters, sink, stream)
+        ms, _, mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph)
+        tflops = flop_per_group * groups * args.steps / (ms * 1e-3) / 1e12
+        out[groups] = (ms / args.steps, tflops)
+        log(f"[bench] MFMA probe, {groups} workgroups x 4 waves x {iters} rounds: {ms / args.steps * 1e3:.2f} us, "
+            f"{tflops:.1f} TFLOP/s, {tflops / groups:.3f} per CU")
+    full, part = out[ncu], out[(3 * ncu) // 4]
+    rec = {"metric": "register-only fp16 MFMA TFLOP/s (v_mfma_f32_32x32x16_f16, one wave per SIMD, every CU)",
+           "value": round(full[1], 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(full[0], 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "fp16 in, fp32 accumulate", "data": "synthetic register operands",
+           "config": {"workload": "mfma", "kind": "probe", "workgroups": ncu, "rounds": iters, "launch": "per step"},
+           "roofline": {"bound": "mfma", "achieved": round(full[1], 2), "peak": FP16_MFMA_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(full[1] / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                        "kernel": "k_mfma_probe"},
+           "three_quarters": {"workgroups": (3 * ncu) // 4, "TFLOPs": round(part[1], 2),
+                              "per_cu_over_all_cus": round((part[1] / ((3 * ncu) // 4)) / (full[1] / ncu), 4)},
+           "cpu_baseline": None}
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -654,6 +715,8 @@ def main() -> int:
         return run_palettize(args, pe, pe.SEEDS.get(args.workload, 1006))
     if kind == "load":
         return run_load(args, pe, pe.SEEDS.get(args.workload, 1007))
+    if kind in ("launch", "mfma"):
+        return run_probe(args, pe, kind)
     if args.batch is not None and kind in ("gemv", "gemm"):
         batch = args.batch  # batch vectors, or the GEMM's rows of X
     seed = pe.SEEDS.get(args.workload, 1000)

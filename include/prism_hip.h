@@ -305,6 +305,17 @@ const void* prism_hip_model_logits_dev(const prism_hip_model* m);
  * `stream` (NULL: the context stream) and returns. */
 int prism_hip_stream_read_dev(prism_hip_ctx* ctx, const void* d_buf, size_t bytes, void* d_sink, void* stream);
 
+/* Two more measuring sticks, no counterpart in the reference either.
+ * prism_hip_launch_empty_dev enqueues one launch of an empty one-wave kernel
+ * (the cost of a dependent launch, which bounds chains of small kernels such
+ * as the decode step).  prism_hip_mfma_probe_dev enqueues `groups` workgroups
+ * of four waves, each wave running `iters` rounds of 16
+ * v_mfma_f32_32x32x16_f16 on registers (524 288 flop per wave and round);
+ * d_sink (>= 1 KB of device memory) is (almost surely) not written.  Both
+ * enqueue on `stream` (NULL: the context stream) and return. */
+int prism_hip_launch_empty_dev(prism_hip_ctx* ctx, void* stream);
+int prism_hip_mfma_probe_dev(prism_hip_ctx* ctx, uint32_t groups, uint32_t iters, void* d_sink, void* stream);
+
 /* The kernels the dispatch launched in the context's most recent compute
  * call (GEMV, gate/up, GEMM, row decode, palettize, read floor), by their
  * device names in launch order, joined by " + ", e.g.

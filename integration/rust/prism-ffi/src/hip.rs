@@ -111,6 +111,10 @@ extern "C" {
     // No reference counterpart: the read floor the GEMVs are measured against
     pub fn prism_hip_stream_read_dev(ctx: *mut prism_hip_ctx, d_buf: *const c_void, bytes: usize,
         d_sink: *mut c_void, stream: *mut c_void) -> c_int;
+    // No reference counterpart: one dependent launch, the matrix cores' rate
+    pub fn prism_hip_launch_empty_dev(ctx: *mut prism_hip_ctx, stream: *mut c_void) -> c_int;
+    pub fn prism_hip_mfma_probe_dev(ctx: *mut prism_hip_ctx, groups: u32, iters: u32, d_sink: *mut c_void,
+        stream: *mut c_void) -> c_int;
     // No reference counterpart: the kernels the last compute call launched
     pub fn prism_hip_last_kernels(ctx: *mut prism_hip_ctx) -> *const c_char;
 }

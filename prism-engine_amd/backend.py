@@ -156,6 +156,14 @@ class Context:
         self.check(self.lib.prism_hip_stream_read_dev(self.h, ptr(d_buf), nbytes, ptr(d_sink),
                                                       _stream_handle(stream)))
 
+    def launch_empty_dev(self, stream=None) -> None:
+        """One launch of an empty kernel (measure_kernels.hpp)."""
+        self.check(self.lib.prism_hip_launch_empty_dev(self.h, _stream_handle(stream)))
+
+    def mfma_probe_dev(self, groups: int, iters: int, d_sink, stream=None) -> None:
+        """`groups` workgroups of register-only MFMA rounds (measure_kernels.hpp)."""
+        self.check(self.lib.prism_hip_mfma_probe_dev(self.h, groups, iters, ptr(d_sink), _stream_handle(stream)))
+
     def gemm_dev(self, w: "Weight", d_X, M: int, d_Y, stream=None) -> None:
         self.check(self.lib.prism_hip_gemm_dev(self.h, w.h, ptr(d_X), M, ptr(d_Y), _stream_handle(stream)))
 

@@ -1571,6 +1571,30 @@ int prism_hip_stream_read_dev(prism_hip_ctx* ctx, const void* d_buf, size_t byte
   return PRISM_HIP_OK;
 }
 
+// ---- measurement: one dependent launch, and the matrix cores' rate
+int prism_hip_launch_empty_dev(prism_hip_ctx* ctx, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
+  PRISM_LAUNCH(prism::k_launch_empty, dim3(1), dim3(64), 0, pick_stream(ctx, stream));
+  HIP_TRY(ctx, hipGetLastError());
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
+int prism_hip_mfma_probe_dev(prism_hip_ctx* ctx, uint32_t groups, uint32_t iters, void* d_sink, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  if (!d_sink) return fail(ctx, PRISM_HIP_ERR_NULL, "sink is NULL");
+  if (groups == 0 || groups > 65536) return fail(ctx, PRISM_HIP_ERR_SIZE, "%u workgroups: 1..65536", groups);
+  DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
+  PRISM_LAUNCH(prism::k_mfma_probe, dim3(groups), dim3(256), 0, pick_stream(ctx, stream), iters,
+               reinterpret_cast<float*>(d_sink));
+  HIP_TRY(ctx, hipGetLastError());
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
 }  // extern "C"
 
 // GPU-resident decode step (prism_hip_model_*).
