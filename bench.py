@@ -50,11 +50,14 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FP16_MFMA_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
-# HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 1.99904 + WRITE_SIZE x 1,
-# scales from a 64 MiB copy), by (workload, batch): (bytes, the kernel the profile
-# measured, the profile).  A line carries the figure only when the library reports
-# that the same kernel ran.
-PMC_TRAFFIC = {("hero", 1): (30110612, "k_gemv_lpr<8, 1, 1, 0, 16>", "profiles/k_gemv_lpr_hero_4bit_b1.md")}
+# HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x 1.999 + WRITE_SIZE x 1,
+# scales from a 64 MiB copy in the same run), by (workload, batch): (bytes, the kernel
+# the profile measured, the profile).  A line carries the figure only when the
+# library reports that the same kernel ran.
+PMC_TRAFFIC = {
+    ("hero", 1): (30110612, "k_gemv_lpr<8, 1, 1, 0, 16>", "profiles/k_gemv_lpr_hero_4bit_b1.md"),
+    ("cfg2", 1): (69368052, "k_gemv_lpr_hg<8, 2, 1, 1, 14>", "profiles/k_gemv_lpr_hg_cfg2_gateup_swiglu.md"),
+}
 
 WORKLOADS = {
     # name: (kind, bits, N, K, batch/M)

@@ -84,19 +84,36 @@ constexpr int kLprFirst = 5;
 constexpr int kLprAhead = 5;
 constexpr int kLprXBlock = 2;
 
-template <int S, int NM, int NB, int EPI, int NCH = 0>
+// HG (half-groups, G = 32): lanes 0..31 and 32..63 of every wave take the 32
+// rows of two different groups, each lane still one row, all 64 tables in
+// one bank-private set: NM = 2, group g of the gate matrix in lanes 0..31
+// and group g of the up matrix in lanes 32..63 (workgroup g), so gate and up
+// of the same rows meet in one workgroup with one 64 KB table set; NM = 1,
+// groups 2g and 2g + 1 of one matrix (workgroup g).  Used where a matrix has
+// more than 64 rows per CU (64 KB of tables per 64 rows: two workgroups per
+// CU fill the LDS).  With NM = 2 the two matrices may lie anywhere, so
+// the loads are global loads from a per-lane 64-bit pointer (lanes 0..31
+// the gate matrix, 32..63 the up matrix) instead of buffer loads: every
+// lane's row exists in memory (the last group is zero-padded), and a
+// chunk load past the wave's range (the run-time loop's last ring slots)
+// re-reads the lane's first chunk instead of relying on the range check.
+// (One buffer descriptor per matrix, each load issued twice with the other
+// half's offsets out of range, took 19.6 against 13.9 us on config 2.)
+template <int S, int NM, int NB, int EPI, int NCH = 0, bool HG = false>
 __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   static_assert(S == 4 || S == 8 || S == 16, "waves per group");
   static_assert(NM == 1 || NM == 2, "one matrix or gate + up");
   static_assert(NB == 1 || NB == 2, "batch vectors per pass");
   static_assert(EPI == kLprPlain || (NM == 2 && NB == 1), "gate/up epilogues are single-vector");
+  constexpr int NT = HG ? 1 : NM;  // table sets (64 KB each) and per-lane streams
+  constexpr bool SPLIT = HG && NM == 2;  // lanes 0..31 and 32..63 in two matrices
   // x chunks per scalar block (16 SGPRs per chunk and vector).  Chunk loads:
   // a ring of R slots (chunk c in slot c % R), chunk c + DR requested once
   // chunk c's table addresses are formed.  NCH = 0 (chunks per wave known at
   // run time): R = DR = XB, a loop over x blocks; NCH > 0 (the host launches
   // it only when the wave's chunk count is NCH): kLprFirst / kLprAhead, one
   // straight-line sequence.
-  constexpr int XB = NCH > 0 ? kLprXBlock : (NM == 1 && NB == 1) ? 4 : 2;
+  constexpr int XB = NCH > 0 ? kLprXBlock : (NT == 1 && NB == 1) ? 4 : 2;
   constexpr int R = NCH == 0 ? XB : (NCH < kLprFirst ? NCH : kLprFirst);
   constexpr int DR = NCH == 0 ? XB : (R < kLprAhead ? R : kLprAhead);
   constexpr int LO = 16 / S;  // low nibbles of the table entries a thread builds
@@ -104,24 +121,62 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
   // static LDS: the tables' address is a link-time constant, so a lookup
   // needs no per-read add
-  __shared__ uint32_t lds[NM * kLprTableDw + S * NM * NB * 64];
-  float* red = reinterpret_cast<float*>(lds + NM * kLprTableDw);
+  __shared__ uint32_t lds[NT * kLprTableDw + S * NT * NB * 64];
+  float* red = reinterpret_cast<float*>(lds + NT * kLprTableDw);
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t g = blockIdx.x;
   const uint32_t N = a.N, K = a.K, NC = K / 32;
   const uint32_t G = a.G;
-  const uint32_t row = g * G + lane;
-  const bool live = lane < G;
   const uint32_t c0 = (w * NC) / S, nch = ((w + 1) * NC) / S - c0;
   const uint32_t gbytes = G * 32u + G * (K / 2);
-  const uint32_t gbase = g * gbytes;
-  __amdgpu_buffer_rsrc_t ri[NM];
   const uint32_t nbytes = ((N + G - 1) / G) * gbytes;
+  // the lane's group, its row in the group and the group's byte offset
+  // from the descriptor's base
+  uint32_t g, lr, gbase;
+  bool live;
+  __amdgpu_buffer_rsrc_t ri[NT];  // SPLIT: unused
+  if constexpr (!HG) {
+    g = blockIdx.x;
+    lr = lane;
+    live = lane < G;
+    gbase = g * gbytes;
 #pragma unroll
-  for (int m = 0; m < NM; m++)
-    ri[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(m == 0 ? a.w : a.w2), (short)0, (int)nbytes, kBufferWord3);
+    for (int m = 0; m < NM; m++)
+      ri[m] = __builtin_amdgcn_make_buffer_rsrc((void*)(m == 0 ? a.w : a.w2), (short)0, (int)nbytes, kBufferWord3);
+  } else if constexpr (NM == 1) {
+    // groups 2 blockIdx.x and 2 blockIdx.x + 1; one past the last group
+    // reads zeros (its offsets are past the range) and stores nothing
+    g = 2 * blockIdx.x + (lane >> 5);
+    lr = lane & 31;
+    live = true;
+    gbase = g * gbytes;
+    ri[0] = __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)nbytes, kBufferWord3);
+  } else {
+    // group blockIdx.x of the gate matrix (lanes 0..31) and of the up
+    // matrix (lanes 32..63)
+    g = blockIdx.x;
+    lr = lane & 31;
+    live = true;
+    gbase = g * gbytes;
+  }
+  const uint32_t row = g * G + lr;
+  // SPLIT: the lane's matrix, addressed per lane
+  const uint8_t* const lp = SPLIT ? (lane >= 32 ? a.w2 : a.w) : nullptr;
+  // 16-byte load of stream m at offset o (LUT loads: default policy; index
+  // chunks: nontemporal)
+  auto ld_lut = [&](int m, uint32_t o) -> u32x4v {
+    if constexpr (SPLIT)
+      return *reinterpret_cast<const u32x4v*>(lp + o);
+    else
+      return __builtin_amdgcn_raw_buffer_load_b128(ri[m], o, 0u, 0);
+  };
+  auto ld_idx = [&](int m, uint32_t o) -> u32x4v {
+    if constexpr (SPLIT)
+      return __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(lp + o));
+    else
+      return __builtin_amdgcn_raw_buffer_load_b128(ri[m], o, 0u, kNontemporal);
+  };
 
   // ---- the LUT of the lane's row: 8 dwords, two 16-byte loads and nothing
   // else (the table build waits for them: a separate load of the low-nibble
@@ -129,12 +184,12 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   // of these registers below).  Lanes past N read the zero LUT slots of the
   // last group's padding rows; lanes past G get an offset past the buffer's
   // range and read zeros.
-  uint32_t L[NM][8];
-  const uint32_t lo = live ? gbase + lane * 32u : 0x80000000u;
+  uint32_t L[NT][8];
+  const uint32_t lo = live ? gbase + lr * 32u : 0x80000000u;
 #pragma unroll
-  for (int m = 0; m < NM; m++) {
-    const u32x4v l0 = __builtin_amdgcn_raw_buffer_load_b128(ri[m], lo, 0u, 0);
-    const u32x4v l1 = __builtin_amdgcn_raw_buffer_load_b128(ri[m], lo + 16u, 0u, 0);
+  for (int m = 0; m < NT; m++) {
+    const u32x4v l0 = ld_lut(m, lo);
+    const u32x4v l1 = ld_lut(m, lo + 16u);
     L[m][0] = l0.x; L[m][1] = l0.y; L[m][2] = l0.z; L[m][3] = l0.w;
     L[m][4] = l1.x; L[m][5] = l1.y; L[m][6] = l1.z; L[m][7] = l1.w;
   }
@@ -145,12 +200,12 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   // buffer's range, which the range check turns into zeros without a
   // memory access.
   const uint32_t cstride = G * kGiChunk;  // bytes from chunk c to c + 1 of a row
-  const uint32_t vbase = live ? gbase + G * 32u + (c0 * G + lane) * kGiChunk : 0x80000000u;
-  u32x4v ring[R][NM];
-  auto ldc = [&](uint32_t i, u32x4v (&dst)[NM]) {
-    const uint32_t vo = i < nch ? vbase + i * cstride : 0x80000000u;
+  const uint32_t vbase = live ? gbase + G * 32u + (c0 * G + lr) * kGiChunk : 0x80000000u;
+  u32x4v ring[R][NT];
+  auto ldc = [&](uint32_t i, u32x4v (&dst)[NT]) {
+    const uint32_t vo = i < nch ? vbase + i * cstride : SPLIT ? vbase : 0x80000000u;
 #pragma unroll
-    for (int m = 0; m < NM; m++) dst[m] = __builtin_amdgcn_raw_buffer_load_b128(ri[m], vo, 0u, kNontemporal);
+    for (int m = 0; m < NT; m++) dst[m] = ld_idx(m, vo);
   };
 #pragma unroll
   for (int u = 0; u < R; u++) ldc(u, ring[u]);
@@ -174,9 +229,9 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   // ---- bank-private pair tables.  The wave builds entries e = w + S i:
   // low nibble w + S (i % LO), high nibble i / LO.  Its LO low-nibble fp16
   // values are LUT entries w + S j, selected from L with the wave-uniform w.
-  uint32_t hv[NM][LO];
+  uint32_t hv[NT][LO];
 #pragma unroll
-  for (int m = 0; m < NM; m++)
+  for (int m = 0; m < NT; m++)
 #pragma unroll
     for (int j = 0; j < LO; j++) {
       const uint32_t e = w + S * j;
@@ -186,7 +241,7 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
       hv[m][j] = (e & 1) ? (d >> 16) : (d & 0xFFFFu);
     }
 #pragma unroll
-  for (int m = 0; m < NM; m++)
+  for (int m = 0; m < NT; m++)
 #pragma unroll
     for (int i = 0; i < 256 / S; i++) {
       const int hi = i / LO;
@@ -200,15 +255,15 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   // entry `xu`; with `refill`, chunk c + DR is requested into its slot once
   // chunk c's table addresses are formed.
   const uint32_t lanebase = lane * 4u;
-  float acc[NM][NB][2];
+  float acc[NT][NB][2];
 #pragma unroll
-  for (int m = 0; m < NM; m++)
+  for (int m = 0; m < NT; m++)
 #pragma unroll
     for (int b = 0; b < NB; b++) acc[m][b][0] = acc[m][b][1] = 0.0f;
   auto chunk = [&](uint32_t c, int slot, int xu, bool refill) {
-    uint32_t pr[NM][16];
+    uint32_t pr[NT][16];
 #pragma unroll
-    for (int m = 0; m < NM; m++)
+    for (int m = 0; m < NT; m++)
 #pragma unroll
       for (int j = 0; j < 16; j++) {
         const uint32_t ad = __builtin_amdgcn_perm(ring[slot][m][j >> 2], lanebase, 0x0C0C0000u | ((4u + (j & 3)) << 8));
@@ -216,7 +271,7 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
       }
     if (refill) ldc(c + DR, ring[(slot + DR) % R]);
 #pragma unroll
-    for (int m = 0; m < NM; m++)
+    for (int m = 0; m < NT; m++)
 #pragma unroll
       for (int b = 0; b < NB; b++)
 #pragma unroll
@@ -249,20 +304,31 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
 
   // ---- wave partials -> LDS -> rows (waves 0 .. NB-1 finish one vector each)
 #pragma unroll
-  for (int m = 0; m < NM; m++)
+  for (int m = 0; m < NT; m++)
 #pragma unroll
-    for (int b = 0; b < NB; b++) red[((w * NM + m) * NB + b) * 64 + lane] = acc[m][b][0] + acc[m][b][1];
+    for (int b = 0; b < NB; b++) red[((w * NT + m) * NB + b) * 64 + lane] = acc[m][b][0] + acc[m][b][1];
   __syncthreads();
   if (w < (uint32_t)NB) {
     const uint32_t b = w;
-    float s[NM];
+    float s[NT];
 #pragma unroll
-    for (int m = 0; m < NM; m++) {
+    for (int m = 0; m < NT; m++) {
       s[m] = 0.0f;
 #pragma unroll
-      for (int v = 0; v < S; v++) s[m] += red[((v * NM + m) * NB + b) * 64 + lane];
+      for (int v = 0; v < S; v++) s[m] += red[((v * NT + m) * NB + b) * 64 + lane];
     }
-    if (live && row < N && b < a.nb) {
+    if constexpr (HG && NM == 2) {
+      // lane r < 32: the gate row's sum; lane r + 32: the same row's up sum,
+      // added in the same wave order
+      if constexpr (EPI == kLprSwiglu) {
+        float su = 0.0f;
+#pragma unroll
+        for (int v = 0; v < S; v++) su += red[v * 64 + (lane ^ 32u)];
+        if (lane < 32 && row < N) store_out(a.y + row, swiglu_h(s[0], su));
+      } else if (row < N) {
+        store_out((lane < 32 ? a.y : a.y2) + row, f2h(s[0]));
+      }
+    } else if (live && row < N && b < a.nb) {
       if constexpr (EPI == kLprSwiglu)
         store_out(a.y + row, swiglu_h(s[0], s[1]));
       else if constexpr (EPI == kLprPair) {
@@ -279,6 +345,15 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr(const uint8_t* w, const uin
                                                      uint16_t* y, uint16_t* y2, uint32_t N, uint32_t K,
                                                      uint32_t nb, uint32_t G) {
   lpr_body<S, NM, NB, EPI, NCH>(lpr_args(w, w2, x, y, y2, N, K, nb, G));
+}
+
+// The half-group form (HG above; G = 32): NM = 2 over ceil(N/32) workgroups,
+// NM = 1 over ceil(N/64).
+template <int S, int NM, int NB, int EPI, int NCH = 0>
+__global__ __launch_bounds__(64 * S) void k_gemv_lpr_hg(const uint8_t* w, const uint8_t* w2, const uint16_t* x,
+                                                        uint16_t* y, uint16_t* y2, uint32_t N, uint32_t K,
+                                                        uint32_t nb, uint32_t G) {
+  lpr_body<S, NM, NB, EPI, NCH, true>(lpr_args(w, w2, x, y, y2, N, K, nb, G));
 }
 
 // Chunk loads of k_gemv_lpr8 when the wave's chunk count is a compile-time

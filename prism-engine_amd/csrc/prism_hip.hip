@@ -459,19 +459,34 @@ hipStream_t pick_stream(prism_hip_ctx* ctx, void* stream) {
 // 0 for split-block.  MI355X, against k_gemv_tile on split-block weights:
 // 14336 x 4096 6.7 (64-row groups, 224 of them) against 8.4 us, gate + up
 // 2 x 14336 x 4096 12.3 us; 4864 x 896 3.5 against 3.05 us and 896 x 4864
-// 6.3 against 3.2 us (too few rows), 2 x 18944 x 3584 19.6 against 17.6 us
-// (more than 64 rows per CU: two rounds), so those stay split-block.
+// 6.3 against 3.2 us (too few rows).
+// 4-bit matrices with more than 64 rows per CU, up to 128 (N <= 32768 on 256
+// CUs), take 32-row groups and the half-group kernels (gemv_lpr.hpp, HG): a
+// workgroup's 64 lanes hold two 32-row groups, two workgroups per CU.
+// MI355X, 2 x 18944 x 3584 gate + up (592 workgroups of 32 + 32 rows):
+// 13.8 us against 16.2-17.1 on split-block weights and 18.8 with 64-row
+// groups (one gate + up workgroup per CU: 296 of them, two rounds); the
+// one-matrix 18944 x 3584 GEMV 8.7 against 9.4 us.
 // 8-bit matrices take the same groups when K % 512 == 0 (k_gemv_lpr8's
 // eight waves split a row into whole blocks of four 16-byte chunks):
 // 14336 x 4096 at 1 / 2 / 4 / 8 vectors 11.8 / 12.1 / 13.6 / 18.2 us
-// against 14.3 / 15.5 / 18.2 / 19.8 on split-block weights.
+// against 14.3 / 15.5 / 18.2 / 19.8 on split-block weights; more than 64
+// rows per CU stay split-block.
 uint32_t gi_rows(const prism_hip_ctx* ctx, uint32_t dm, uint32_t dn, uint32_t bits) {
   if (dn < 2048 || (bits == 4 && dn % 64 != 0) || (bits == 8 && dn % 512 != 0) || (bits != 4 && bits != 8))
     return 0;
   const uint32_t ncu = (uint32_t)ctx->num_cu;
-  const uint32_t G = ((dm + ncu - 1) / ncu + 7) / 8 * 8;
+  uint32_t G = ((dm + ncu - 1) / ncu + 7) / 8 * 8;
+  if (bits == 4 && G > (uint32_t)prism::kGiMaxRows && (dm + 63) / 64 <= 2 * ncu) G = 32;
   if (G < 32 || G > (uint32_t)prism::kGiMaxRows || prism::gi_bytes(G, dm, dn, bits) >= (1ull << 31)) return 0;
   return G;
+}
+
+// 4-bit GI weights run by the half-group kernels: 32-row groups, more of
+// them than CUs (the 32-row groups of N <= 8192 run one group per
+// workgroup, lanes 32..63 idle, so that every CU has one).
+bool gi_half_groups(const prism_hip_ctx* ctx, const prism_hip_weight* w) {
+  return w->bits == 4 && w->gi == 32 && (w->dim_m + 31) / 32 > (uint32_t)ctx->num_cu;
 }
 
 // ---------------------------------------------------------------- GEMV plan
@@ -725,6 +740,24 @@ void launch_lpr(dim3 groups, hipStream_t st, const prism::LprArgs& a) {
     PRISM_LAUNCH((prism::k_gemv_lpr<S, NM, NB, EPI>), groups, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
 }
 
+// The half-group form (G = 32), with a compile-time chunk count as above,
+// and also for 14 chunks per wave (K = 3584 at 8 waves, config 2's rows:
+// gate + up 13.8 against 14.55 us for the run-time loop, MI355X; 16 waves
+// 16.6, and 15.3-15.4 with 7 compile-time chunks each).
+template <int S, int NM, int NB, int EPI>
+void launch_lpr_hg(dim3 grid, hipStream_t st, const prism::LprArgs& a) {
+  const uint32_t NC = a.K / 32;
+  const uint32_t nch = NC % S == 0 ? NC / S : 0;
+  if (nch == 16)
+    PRISM_LAUNCH((prism::k_gemv_lpr_hg<S, NM, NB, EPI, 16>), grid, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
+  else if (nch == 14)
+    PRISM_LAUNCH((prism::k_gemv_lpr_hg<S, NM, NB, EPI, 14>), grid, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
+  else if (nch == 8)
+    PRISM_LAUNCH((prism::k_gemv_lpr_hg<S, NM, NB, EPI, 8>), grid, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
+  else
+    PRISM_LAUNCH((prism::k_gemv_lpr_hg<S, NM, NB, EPI>), grid, dim3(64 * S), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
+}
+
 // 8-bit GI weights: k_gemv_lpr8 with the wave's chunk count as a
 // compile-time constant when it is 16, 32 or 64 (K = 2048 / 4096 / 8192),
 // else the loop over 4-chunk blocks.  Eight vectors a pass only with a
@@ -853,6 +886,7 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
   const bool aligned = reinterpret_cast<uintptr_t>(d_x) % 16 == 0;
   const uint32_t G = w->gi;
   const dim3 groups((N + G - 1) / G);
+  const bool hg = gi_half_groups(ctx, w);
   if (w2) {
     if (aligned) {
       prism::LprArgs a{};
@@ -867,7 +901,12 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.nb = 1;
       // the pair form splits K over the waves as the one-matrix GEMV does
       // (8 waves), so each output is that GEMV's bit for bit
-      if (d_y2)
+      if (hg) {
+        if (d_y2)
+          launch_lpr_hg<8, 2, 1, prism::kLprPair>(groups, st, a);
+        else
+          launch_lpr_hg<8, 2, 1, prism::kLprSwiglu>(groups, st, a);
+      } else if (d_y2)
         launch_lpr<8, 2, 1, prism::kLprPair>(groups, st, a);
       else
         launch_lpr<16, 2, 1, prism::kLprSwiglu>(groups, st, a);
@@ -925,7 +964,13 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.N = N;
       a.K = K;
       a.nb = chunk = left >= 2 ? 2u : 1u;
-      if (chunk == 2)
+      if (hg) {
+        const dim3 pairs((groups.x + 1) / 2);
+        if (chunk == 2)
+          launch_lpr_hg<8, 1, 2, prism::kLprPlain>(pairs, st, a);
+        else
+          launch_lpr_hg<8, 1, 1, prism::kLprPlain>(pairs, st, a);
+      } else if (chunk == 2)
         launch_lpr<8, 1, 2, prism::kLprPlain>(groups, st, a);
       else
         launch_lpr<8, 1, 1, prism::kLprPlain>(groups, st, a);

@@ -56,6 +56,8 @@ def gi_rows(N, K, num_cu=256, bits=4):
     if K < 2048 or K % (64 if bits == 4 else 512):
         return 0
     G = (-(-N // num_cu) + 7) // 8 * 8
+    if bits == 4 and G > GI_MAX and -(-N // 64) <= 2 * num_cu:
+        G = 32
     return G if 32 <= G <= GI_MAX else 0
 
 
@@ -242,6 +244,61 @@ def test_gemv_lpr_offsets(N, K):
                     perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr chunk")
                     assert (perf == ((lane < G) & (i < nch))).all()
                     assert ((vo + 16) <= base + gi_group_bytes(G, K))[perf].all()
+
+
+@pytest.mark.parametrize("N,K", [(18944, 3584), (16416, 2048), (32768, 4096), (16416, 2560)])
+@pytest.mark.parametrize("NM", [1, 2])
+def test_gemv_lpr_hg_offsets(N, K, NM):
+    """k_gemv_lpr_hg (gemv_lpr.hpp, HG): 32-row groups, lanes 0..31 and
+    32..63 in two groups.  NM = 1: groups 2b and 2b + 1 of one matrix under
+    one buffer descriptor (one past the last group reads nothing); NM = 2:
+    group b of the gate matrix (lanes 0..31) and of the up matrix (lanes
+    32..63) through per-lane global loads, so every load the kernel issues
+    (a chunk past the wave's range re-reads the lane's first chunk) must be
+    inside the lane's own matrix, group and row."""
+    G = gi_rows(N, K)
+    assert G == 32
+    S, NC = 8, K // 32
+    gb = gi_group_bytes(G, K)
+    groups = -(-N // G)
+    nbytes = groups * gb
+    assert nbytes == gi_bytes(G, N, K) and nbytes <= 1 << 31
+    lane = np.arange(64)
+    h, lr = lane >> 5, lane & 31
+    blocks = (0, -(-groups // 2) - 1) if NM == 1 else (0, groups - 1)
+    for b in blocks:
+        g = 2 * b + h if NM == 1 else np.full(64, b)
+        gbase = g * gb
+        exists = g < groups
+        past = 0x80000000 if NM == 1 else None  # NM = 2: no range check; past the range -> chunk c0
+        lut = gbase + lr * 32
+        for off in (0, 16):
+            vo = lut + off
+            if NM == 1:
+                perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr_hg LUT")
+                assert (perf == exists).all()
+            else:
+                perf = np.ones(64, dtype=bool)
+                assert ((vo >= 0) & (vo + 16 <= nbytes)).all(), "global LUT load outside the matrix"
+            assert ((vo + 16) <= gbase + (lr + 1) * 32)[perf].all(), "LUT load leaves its row"
+        for w in range(S):
+            c0, nch = (w * NC) // S, ((w + 1) * NC) // S - (w * NC) // S
+            vbase = gbase + G * 32 + (c0 * G + lr) * GI_CHUNK
+            for i in range(nch + 8):
+                if i < nch:
+                    vo = vbase + i * G * GI_CHUNK
+                else:
+                    vo = np.full(64, past) if NM == 1 else vbase
+                if NM == 1:
+                    perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr_hg chunk")
+                    assert (perf == (exists & (i < nch))).all()
+                else:
+                    perf = np.ones(64, dtype=bool)
+                    assert ((vo >= 0) & (vo + 16 <= nbytes)).all(), "global chunk load outside the matrix"
+                assert ((vo >= gbase) & ((vo + 16) <= gbase + gb))[perf].all(), "chunk load leaves its group"
+                q = (vo - gbase - G * 32) // GI_CHUNK
+                c_is = np.where(i < nch, c0 + i, c0)  # the re-read past the range is chunk c0
+                assert ((q % G == lr) & (q // G == c_is))[perf].all()
 
 
 @pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (16384, 2048), (8192, 2560)])

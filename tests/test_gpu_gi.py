@@ -10,9 +10,14 @@ generic kernel (unaligned x), the GEMM, the row decode and the decode-step
 model's copies.  4-bit shapes (on a 256-CU MI355X): 14336 x 4096 (56-row
 groups, 256 of them), 9100 x 2048 (40-row groups, 228 with a ragged last
 one), 8192 x 2112 (32-row groups; K % 128 != 0: no matrix-core pass),
-16384 x 2048 (64-row groups).  8-bit shapes: 14336 x 4096 and 9100 x 2048
-(chunk counts the 8-bit kernel takes as compile-time constants), 8192 x
-2560 (its loop form), 16384 x 2048.
+16384 x 2048 (64-row groups); more than 64 rows per CU take 32-row groups
+and the half-group kernels (two groups, or gate and up of one group, in the
+two halves of a wave): 18944 x 3584 (config 2's matrices: 592 groups, 14
+chunks per wave), 16416 x 2048 and 16416 x 2560 (513 groups: the last
+workgroup's second half is past the matrix; 8 chunks per wave, and 10:
+the run-time chunk loop).  8-bit shapes:
+14336 x 4096 and 9100 x 2048 (chunk counts the 8-bit kernel takes as
+compile-time constants), 8192 x 2560 (its loop form), 16384 x 2048.
 """
 import numpy as np
 import pytest
@@ -20,7 +25,9 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
-GI_SHAPES = [(14336, 4096), (9100, 2048), (8192, 2112), (16384, 2048)]
+GI_SHAPES = [(14336, 4096), (9100, 2048), (8192, 2112), (16384, 2048), (18944, 3584), (16416, 2048),
+             (16416, 2560)]
+HG_SHAPES = [(18944, 3584), (16416, 2560)]  # 32-row groups, half-group kernels
 
 
 def _rel(y, ref):
@@ -43,6 +50,8 @@ def _gi(N, K, bits=4, num_cu=256):
     if K < 2048 or bits not in (4, 8) or K % (64 if bits == 4 else 512):
         return 0
     G = (-(-N // num_cu) + 7) // 8 * 8
+    if bits == 4 and G > 64 and -(-N // 64) <= 2 * num_cu:
+        G = 32
     return G if 32 <= G <= 64 else 0
 
 
@@ -113,7 +122,7 @@ def test_gi_lpr_x_on_16_byte_boundary(pe, oracle, gpu_ctx, nb):
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (16416, 2048)])
 def test_gi_unaligned_x(pe, oracle, gpu_ctx, N, K):
     """x not 16-byte aligned: the generic kernel reads GI as well."""
     import torch
@@ -131,7 +140,7 @@ def test_gi_unaligned_x(pe, oracle, gpu_ctx, N, K):
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (16416, 2048)])
 def test_gi_decode_rows(pe, oracle, gpu_ctx, N, K):
     """Row decode and lut_embed over GI are the oracle's bytes exactly,
     including rows of the ragged last group."""
@@ -150,7 +159,7 @@ def test_gi_decode_rows(pe, oracle, gpu_ctx, N, K):
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (16416, 2048)])
 def test_gi_upload_dev(pe, gpu_ctx, N, K):
     """A device-side payload is regrouped the same way as a host one."""
     import torch
@@ -168,7 +177,8 @@ def test_gi_upload_dev(pe, gpu_ctx, N, K):
 # per workgroup, 8-bit), config 2's matrix, ragged K (generic kernel), and
 # GI shapes (the lane-per-row kernel's pair form)
 PAIR_SHAPES = [(4, 4864, 896), (4, 18944, 3584), (4, 300, 4096), (8, 300, 512), (8, 14336, 4096),
-               (4, 7, 40), (8, 9, 7), (4, 14336, 4096), (4, 9100, 2048)]
+               (4, 7, 40), (8, 9, 7), (4, 14336, 4096), (4, 9100, 2048), (4, 16416, 2048),
+               (4, 16416, 2560)]
 
 
 @pytest.mark.parametrize("bits,N,K", PAIR_SHAPES)
@@ -218,7 +228,7 @@ def test_gate_up_pair_dev_and_errors(pe, gpu_ctx):
         w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)] + HG_SHAPES)
 def test_gi_gateup_swiglu(pe, oracle, gpu_ctx, N, K):
     tg = pe.synth_tensor(N, K, 4, seed=N + 5)
     tu = pe.synth_tensor(N, K, 4, seed=N + 6)
@@ -231,18 +241,20 @@ def test_gi_gateup_swiglu(pe, oracle, gpu_ctx, N, K):
     wu.free()
 
 
-@pytest.mark.parametrize("M", [24, 64, 200, 300])
-def test_gi_gemm(pe, oracle, gpu_ctx, M):
-    """Prefill GEMM over GI weights with a ragged last group (40-row groups,
-    so a wave's 64 rows span two of them): GEMV passes (24 rows), split K
-    (64, 200) and whole-K blocks (300); every row checked against the
-    float32 product of the decoded weights, a spread of rows against the
-    oracle."""
-    N, K = 9100, 2048
+@pytest.mark.parametrize("N,M", [(9100, 24), (9100, 64), (9100, 200), (9100, 300), (16416, 24), (16416, 64),
+                                 (16416, 300)])
+def test_gi_gemm(pe, oracle, gpu_ctx, N, M):
+    """Prefill GEMM over GI weights with a ragged last group (9100: 40-row
+    groups, so a wave's 64 rows span two of them; 16416: 32-row groups, the
+    last one half full): GEMV passes (24 rows), split K (64, 200) and
+    whole-K blocks (300); every row checked against the float32 product of
+    the decoded weights, a spread of rows against the oracle."""
+    K = 2048
+    assert _gi(N, K)
     t = pe.synth_tensor(N, K, 4, seed=M + 40)
     X = pe.synth_x(M, K, seed=M + 41)
     w = gpu_ctx.upload_tensor(t)
-    print(f"gi gemm M={M}", flush=True)
+    print(f"gi gemm {N}x{K} M={M}", flush=True)
     Y = gpu_ctx.gemm(w, X)
     dense = oracle.decode_rows(t.payload, N, K, 4, 0, N).view(np.float16).astype(np.float32)
     Yf = X.view(np.float16).astype(np.float32) @ dense.T
@@ -257,11 +269,13 @@ def test_gi_gemm(pe, oracle, gpu_ctx, M):
     w.free()
 
 
-def test_gi_model_step(pe, oracle, gpu_ctx):
+@pytest.mark.parametrize("inter", [8192, 16416])
+def test_gi_model_step(pe, oracle, gpu_ctx, inter):
     """A decode-step model whose embedding (9000 x 2048) and gate/up
-    (8192 x 2048) weights were uploaded in the GI layout: the model's
-    split-block copies are regrouped back, and the step matches the oracle."""
-    cfg = pe.Qwen2Config(n_layers=1, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64, intermediate=8192,
+    (8192 or 16416 x 2048: 32-row groups, the second in half-group form)
+    weights were uploaded in the GI layout: the model's split-block copies
+    are regrouped back, and the step matches the oracle."""
+    cfg = pe.Qwen2Config(n_layers=1, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64, intermediate=inter,
                          vocab=9000)
     assert _gi(cfg.vocab, cfg.hidden) and _gi(cfg.intermediate, cfg.hidden)
     embed, layers = pe.synth_weights(cfg, 21)
@@ -301,7 +315,7 @@ def test_gi8_gemv(pe, oracle, gpu_ctx, N, K, batch):
     w.free()
 
 
-@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (8192, 2112)])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (8192, 2112)] + HG_SHAPES)
 def test_gi4_decode_bit_exact_through_lpr(pe, gpu_ctx, N, K):
     """One-hot x through the 4-bit lane-per-row GEMV (one vector): every
     output is LUT_r[idx(r, k)] exactly.  k runs over every element of the
@@ -309,7 +323,8 @@ def test_gi4_decode_bit_exact_through_lpr(pe, gpu_ctx, N, K):
     chunks per wave the kernel's chunk sequence is compile-time) and the
     last 64 elements of the row (the last wave's last products, summed right
     after the chunk sequence); 2112 (66 chunks, not a multiple of 8 waves)
-    takes the run-time loop."""
+    and 2560 (10 chunks per wave) take the run-time loop.  The half-group
+    shapes check both halves of every wave (rows of two groups)."""
     assert _gi(N, K)
     t = pe.synth_tensor(N, K, 4, seed=K + 29)
     lut, idx = pe.unpack_payload(t.payload, N, K, 4)
