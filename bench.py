@@ -422,7 +422,7 @@ def run_decode(args, pe, seed) -> int:
                    "vocab": cfg.vocab, "kv_len": L0, "launch": "one HIP graph per token", "seed": seed},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode step (embed + 5 launches per layer + LM head, one graph)",
+                     "kernel": "decode step (k_step_begin + one graph: 5 launches per layer + LM head)",
                      "algorithmic_per_launch": step_bytes},
         "cpu_baseline": cpu,
         "parity_rel_err": err,

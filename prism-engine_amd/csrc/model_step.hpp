@@ -17,8 +17,9 @@
 //   activations      residual stream h [hidden], q|k|v [nqkv], attention
 //                    split partials [nh][kAttnSplits][66] fp32, SwiGLU output
 //                    [intermediate], logits [vocab] fp16; StepParams
-// One step = k_step_set_params (token, pos, KV lengths) + one graph replay
-// of the fixed launch sequence (captured once per weight set).
+// One step = k_step_begin (token, pos, KV lengths by value: stores them and
+// the token's embedding row) + one graph replay of the fixed launch
+// sequence (captured once per weight set).
 #pragma once
 #include <cmath>
 #include <vector>
@@ -106,8 +107,6 @@ int model_enqueue(prism_hip_model* m, hipStream_t st) {
   const uint32_t D = c.hidden, I = c.intermediate, V = c.vocab;
   const float eps = c.rms_eps;
   int rc;
-  hipLaunchKernelGGL(prism::k_step_embed, dim3(1), dim3(256), 0, st, m->embed, V, D, m->d_params, m->hres);
-  HIP_TRY(ctx, hipGetLastError());
   for (uint32_t l = 0; l < c.n_layers; l++) {
     const uint8_t* wq = m->qkv[l];
     if ((rc = launch_gemv_raw(ctx, 4, m->nqkv, D, wq, wq + (size_t)m->nqkv * 32, nullptr, nullptr, m->hres, 1,
@@ -414,7 +413,8 @@ int prism_hip_model_step_dev(prism_hip_model* m, uint32_t token, int64_t pos, vo
     m->graph = gr;
     HIP_TRY(ctx, hipGraphInstantiate(&m->exec, m->graph, nullptr, nullptr, 0));
   }
-  hipLaunchKernelGGL(prism::k_step_set_params, dim3(1), dim3(64), 0, st, p, m->d_params);
+  hipLaunchKernelGGL(prism::k_step_begin, dim3(1), dim3(256), 0, st, p, m->d_params, m->embed, c.vocab, c.hidden,
+                     m->hres);
   HIP_TRY(ctx, hipGetLastError());
   HIP_TRY(ctx, hipGraphLaunch(m->exec, st));
   for (uint32_t l = 0; l < c.n_layers; l++) m->kv_len[l] += 1;

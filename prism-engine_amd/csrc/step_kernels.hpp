@@ -1,13 +1,13 @@
 // step_kernels.hpp -- the non-GEMV kernels of the GPU-resident decode step
 // (PrismEngine::step, src/lut/engine_impl.rs:1076-1405, for a Qwen2 graph).
 //
-// Per token the step runs: k_step_embed; per layer the QKV GEMV (RMS norm
+// Per token the step runs: k_step_begin; per layer the QKV GEMV (RMS norm
 // in its prologue), k_step_attention, the O GEMV (+ residual), the gate/up
 // SwiGLU GEMV (RMS norm in its prologue), the down GEMV (+ residual); the
 // LM-head GEMV (RMS norm in its prologue).  Everything that changes from
 // token to token (token id, position, KV lengths) is read from a StepParams
-// block in device memory, so the launch sequence is fixed and replays as
-// one HIP graph.
+// block in device memory, which k_step_begin writes, so the launch sequence
+// after it is fixed and replays as one HIP graph.
 //
 // KV cache: the reference's INT8 cache (KVCache, engine_impl.rs:514-584),
 // kept in HBM as two planes per layer and matrix: int8 values
@@ -29,16 +29,21 @@ struct StepParams {
   uint32_t kv_len[kMaxLayers];  // tokens cached per layer before this step
 };
 
-__global__ void k_step_set_params(StepParams v, StepParams* dst) {
-  if (threadIdx.x == 0) *dst = v;
-}
-
-// Embedding row of the step's token: lut_embed (compute-core/src/lut/
-// evaluator.rs:176-197; engine_impl.rs:1407-1446): LUT[token][nibble] for
-// the first (D/8)*8 elements, zeros past them and for tokens >= vocab.
-__global__ __launch_bounds__(256) void k_step_embed(const uint8_t* __restrict__ emb, uint32_t vocab, uint32_t D,
-                                                    const StepParams* __restrict__ sp, uint16_t* __restrict__ h) {
-  const uint32_t tok = sp->token;
+// The first kernel of a step (launched with the step's parameters by value,
+// ahead of the graph): stores the StepParams block for the graph's kernels
+// and writes the embedding row of the step's token into the residual stream:
+// lut_embed (compute-core/src/lut/evaluator.rs:176-197; engine_impl.rs:
+// 1407-1446): LUT[token][nibble] for the first (D/8)*8 elements, zeros past
+// them and for tokens >= vocab.  (As two kernels, the parameters' store and
+// the embedding as the graph's first node, every token paid one more
+// dependent launch.)
+__global__ __launch_bounds__(256) void k_step_begin(StepParams v, StepParams* __restrict__ dst,
+                                                    const uint8_t* __restrict__ emb, uint32_t vocab, uint32_t D,
+                                                    uint16_t* __restrict__ h) {
+  static_assert(sizeof(StepParams) % 4 == 0, "copied as dwords");
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(&v);
+  for (uint32_t i = threadIdx.x; i < sizeof(StepParams) / 4; i += blockDim.x) reinterpret_cast<uint32_t*>(dst)[i] = src[i];
+  const uint32_t tok = v.token;
   const uint32_t keff = (D / 8) * 8;
   for (uint32_t k = threadIdx.x; k < D; k += blockDim.x) {
     uint16_t v = 0;
