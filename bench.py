@@ -34,6 +34,8 @@ of them: TFLOP/s and the rate per CU).
 from __future__ import annotations
 
 import argparse
+import ctypes
+import dataclasses
 import importlib
 import json
 import os
@@ -276,6 +278,36 @@ def time_launches(launch, steps: int, warmup: int, stream, use_graph: bool, copi
     return e0.elapsed_time(e1), wall * 1e3, ("hip_graph" if use_graph and steps > EAGER_MAX_STEPS else "eager")
 
 
+def time_two_streams(launch, steps: int, warmup: int, s0, s1, copies: int) -> float:
+    """A probe, not the headline: `steps` launches alternating between two
+    streams (launch(i, stream)), so a launch never waits for its neighbour
+    and the start of one can overlap the end of the other.  Eager, behind a
+    device-side spin on s0; the window opens on s0 before the first timed
+    launch (s1 waits for it) and closes on s0 after both streams' last
+    launches.  Returns device ms."""
+    import torch
+    for i in range(copies):
+        launch(i, s0)
+    torch.cuda.synchronize()
+    e0, e1, e_end1 = HipEvent(), HipEvent(), HipEvent()
+    ms = None
+    for rep in range(2):  # the first sequence untimed
+        device_busy(s0, max(10.0, 0.03 * (warmup + steps)))
+        for i in range(warmup):
+            launch(i, s0)
+        e0.record(s0)
+        HipEvent._hip.hipStreamWaitEvent.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint]
+        HipEvent._check(HipEvent._hip.hipStreamWaitEvent(s1.cuda_stream, e0.h, 0), "hipStreamWaitEvent")
+        for i in range(steps):
+            launch(warmup + i, (s0, s1)[i % 2])
+        e_end1.record(s1)
+        HipEvent._check(HipEvent._hip.hipStreamWaitEvent(s0.cuda_stream, e_end1.h, 0), "hipStreamWaitEvent")
+        e1.record(s0)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+    return ms
+
+
 def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
     """The oracle (a C restatement of lut_gemv_cpu, single thread like the
     reference) timed on this host on a bounded sample of the workload."""
@@ -326,10 +358,16 @@ def cpu_baseline(kind, bits, N, K, batch, tensors, x, budget_s=12.0):
 
 
 def run_decode(args, pe, seed) -> int:
-    """Config 3: the GPU-resident decode step (prism_hip_model_step_dev)."""
+    """Config 3: the GPU-resident decode step (prism_hip_model_step_dev).
+    --layers / --vocab shrink the model (a probe of where the weights sit:
+    inside the L2s or the MALL); the headline is the full model."""
     import torch
     oracle = importlib.import_module("oracle")
     cfg = pe.Qwen2Config()
+    if args.layers is not None:
+        cfg = dataclasses.replace(cfg, n_layers=args.layers)
+    if args.vocab is not None:
+        cfg = dataclasses.replace(cfg, vocab=args.vocab)
     L0 = DECODE_KV_LEN
     log(f"[bench] workload=cfg3 decode step: Qwen2.5-0.5B architecture, 4-bit, KV {L0}, seed={seed}")
     embed, layers = pe.synth_weights(cfg, seed)
@@ -405,7 +443,9 @@ def run_decode(args, pe, seed) -> int:
         log(f"[bench] cpu baseline {cpu['value']} tokens/s")
 
     rec = {
-        "metric": "Qwen2.5-0.5B-architecture decode step tokens/s (4-bit palettized, batch 1, KV 512)",
+        "metric": "Qwen2.5-0.5B-architecture decode step tokens/s (4-bit palettized, batch 1, KV 512)"
+                  + ("" if (args.layers is None and args.vocab is None) else
+                     f" -- probe: {cfg.n_layers} layers, vocabulary {cfg.vocab}"),
         "value": round(tps, 2),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -692,6 +732,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-floor", action="store_true", help="skip the same-process read-floor leg")
     ap.add_argument("--rotate-mb", type=int, default=640, help="distinct weight bytes the steps rotate over")
+    ap.add_argument("--streams", type=int, default=1, choices=(1, 2),
+                    help="probe (hero and floor only): 2 alternates the launches between two streams, so "
+                         "neighbouring launches do not wait for each other (the headline is 1: a dependent chain)")
+    ap.add_argument("--layers", type=int, default=None, help="cfg3: decoder layers (default 24)")
+    ap.add_argument("--vocab", type=int, default=None, help="cfg3: vocabulary, the LM head's rows (default 151936)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="after timing, run one untimed device copy of MB MiB (scale reference for "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -712,6 +757,12 @@ def main() -> int:
     import torch
     pe = importlib.import_module("prism-engine_amd")
     kind, bits, N, K, batch = WORKLOADS[args.workload]
+    if args.streams == 2 and not (kind == "floor" or (args.workload == "hero" and (args.batch or 1) == 1)):
+        print(json.dumps({"error": "--streams 2 is a probe for the hero GEMV and the read floor"}))
+        return 2
+    if (args.layers is not None or args.vocab is not None) and kind != "decode":
+        print(json.dumps({"error": "--layers / --vocab apply to cfg3"}))
+        return 2
     if kind == "decode":
         return run_decode(args, pe, pe.SEEDS.get(args.workload, 1003))
     if kind == "palettize":
@@ -739,8 +790,8 @@ def main() -> int:
         sink = torch.zeros(256, dtype=torch.int32, device=dev)
         log(f"[bench] {copies} buffers x {wb / 1e6:.2f} MB = {copies * wb / 1e6:.0f} MB rotated")
 
-        def launch(i: int) -> None:
-            ctx.stream_read_dev(bufs[i % copies], wb, sink, stream)
+        def launch(i: int, st=stream) -> None:
+            ctx.stream_read_dev(bufs[i % copies], wb, sink, st)
         err = None
         args.no_cpu = True
     else:
@@ -750,11 +801,14 @@ def main() -> int:
         dx = torch.from_numpy(x.view(np.int16)).to(dev)
         ny = (batch * N) if kind != "gateup" else N
         dy = torch.empty(ny, dtype=torch.int16, device=dev)
+        dy2 = torch.empty(ny, dtype=torch.int16, device=dev)  # the second stream's output (--streams 2)
         log(f"[bench] {copies} weight copies x {wb / 1e6:.2f} MB = {copies * wb / 1e6:.0f} MB rotated")
 
-        def launch(i: int) -> None:
+        def launch(i: int, st=None) -> None:
             w = weights[i % copies]
-            if kind == "gemv":
+            if st is not None and st is not stream:
+                ctx.gemv_dev(w[0], dx, batch, dy2, st)
+            elif kind == "gemv":
                 ctx.gemv_dev(w[0], dx, batch, dy, stream)
             elif kind == "gateup":
                 ctx.gateup_swiglu_dev(w[0], w[1], dx, dy, stream)
@@ -791,7 +845,12 @@ def main() -> int:
     kernel_name = ctx.last_kernels()
     log(f"[bench] kernels of one step: {kernel_name}")
 
-    ms, wall_ms, launch_mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph, copies)
+    if args.streams == 2:
+        # probe: neighbouring launches independent, on two streams
+        ms = time_two_streams(launch, args.steps, args.warmup, stream, torch.cuda.Stream(device=dev), copies)
+        wall_ms, launch_mode = float("nan"), "eager, two streams (neighbouring launches independent)"
+    else:
+        ms, wall_ms, launch_mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph, copies)
     ms_step = ms / args.steps
     log(f"[bench] timed {args.steps} steps ({launch_mode}, behind a device-side spin): {ms:.3f} ms on device "
         f"events, {wall_ms:.3f} ms wall")
@@ -799,7 +858,7 @@ def main() -> int:
     # the read floor in the same process: k_stream_read over as many bytes
     # per launch, rotated over as many distinct buffers, timed the same way
     floor = None
-    if kind in ("gemv", "gateup") and not args.no_floor:
+    if kind in ("gemv", "gateup") and not args.no_floor and args.streams == 1:
         g = torch.Generator(device=dev).manual_seed(seed + 1)
         fbufs = [torch.randint(0, 256, (wb,), dtype=torch.uint8, device=dev, generator=g) for _ in range(copies)]
         fsink = torch.zeros(256, dtype=torch.int32, device=dev)
@@ -834,7 +893,12 @@ def main() -> int:
         value = wb / (ms_step * 1e-3) / 1e9
         unit = "GB/s"
         metric = ("palettized GEMV effective HBM GB/s (% of 8 TB/s peak), 4-bit, batch 1"
+                  if args.workload == "hero" and batch == 1 and args.streams == 1 else
+                  "palettized GEMV HBM GB/s with neighbouring launches overlapping (two streams; a probe, "
+                  "not the dependent-chain headline), 4-bit, batch 1"
                   if args.workload == "hero" and batch == 1 else
+                  "streaming-read floor GB/s, neighbouring launches overlapping (two streams)"
+                  if kind == "floor" and args.streams == 2 else
                   f"streaming-read floor GB/s (one launch over the {'hero' if bits == 4 else 'config-4'} weight bytes)"
                   if kind == "floor" else
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
@@ -870,7 +934,7 @@ def main() -> int:
                  "synthetic (seeded PCG64: x~N(0,1) fp16, uniform indices, sorted N(0,0.02) fp16 LUTs)"),
         "config": {"workload": args.workload, "kind": kind, "bits": bits, "N": N, "K": K,
                    ("M" if kind == "gemm" else "batch"): batch, "weight_copies_rotated": copies,
-                   "launch": launch_mode, "seed": seed},
+                   "launch": launch_mode, "streams": args.streams, "seed": seed},
         "roofline": roof,
         "floor": floor,
         "cpu_baseline": cpu,
