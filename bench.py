@@ -59,6 +59,7 @@ MALL_BYTES = 256 << 20
 PMC_TRAFFIC = {
     ("hero", 1): (30110612, "k_gemv_lpr<8, 1, 1, 0, 16>", "profiles/k_gemv_lpr_hero_4bit_b1.md"),
     ("cfg2", 1): (69368052, "k_gemv_lpr_hg<8, 2, 1, 1, 14>", "profiles/k_gemv_lpr_hg_cfg2_gateup_swiglu.md"),
+    ("cfg4", 1): (66438202, "k_gemv_lpr8<8, 1, 1, 0, 32>", "profiles/k_gemv_lpr8_cfg4_8bit.md"),
 }
 
 WORKLOADS = {
