@@ -26,7 +26,7 @@ a Qwen2.5-0.5B-architecture model, fp32 N(0, 0.02) weights resident in HBM,
 k=16, max_iter=50 as compile_to_cimage uses: fp32 params/s), floor (the
 read floor the GEMVs are held to: one launch of the library's streaming-read
 kernel over as many bytes as the hero GEMV reads, rotated the same way;
-floor8 the same over config 4's 66 MB), load (a step is one load_cimage of a Qwen2.5-0.5B-sized 4-bit .cimage: mmap,
+floor8 the same over config 4's 66 MB, floor1 over config 1's 2.3 MB), load (a step is one load_cimage of a Qwen2.5-0.5B-sized 4-bit .cimage: mmap,
 every tensor through the pinned staging ring, one wait; GB/s of payload), launch (an empty kernel launched back to
 back: the cost of one dependent launch, us), mfma (register-only matrix-core work on every CU and on three quarters
 of them: TFLOP/s and the rate per CU).
@@ -76,6 +76,8 @@ WORKLOADS = {
     "floor": ("floor", 4, 14336, 4096, 1),
     # the same over config 4's bytes (8-bit 14336 x 4096: 66 MB)
     "floor8": ("floor", 8, 14336, 4096, 1),
+    # and over config 1's (4-bit 4864 x 896: 2.3 MB, a latency-bound launch)
+    "floor1": ("floor", 4, 4864, 896, 1),
     # .cimage -> device: load_cimage of a Qwen2.5-0.5B-sized file
     "load": ("load", 4, 0, 0, 1),
     # measuring sticks: one dependent launch, the matrix cores' rate
@@ -900,7 +902,8 @@ def main() -> int:
                   if args.workload == "hero" and batch == 1 else
                   "streaming-read floor GB/s, neighbouring launches overlapping (two streams)"
                   if kind == "floor" and args.streams == 2 else
-                  f"streaming-read floor GB/s (one launch over the {'hero' if bits == 4 else 'config-4'} weight bytes)"
+                  f"streaming-read floor GB/s (one launch over the "
+                  f"{'config-1' if args.workload == 'floor1' else 'hero' if bits == 4 else 'config-4'} weight bytes)"
                   if kind == "floor" else
                   f"palettized {kind} effective HBM GB/s (% of 8 TB/s peak), {bits}-bit, batch {batch}")
         roof = {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
