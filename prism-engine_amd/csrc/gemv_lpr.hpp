@@ -83,6 +83,13 @@ constexpr int kLprPair = 2;    // NM = 2: y[row] = f16(gate), y2[row] = f16(up)
 constexpr int kLprFirst = 5;
 constexpr int kLprAhead = 5;
 constexpr int kLprXBlock = 2;
+// The half-group form (HG below) runs two workgroups per CU and prefers a
+// shallower ring: config 2 (NCH = 14) 13.58-13.71 us with (4, 4) against
+// 13.68-13.79 with (5, 5), three alternating rounds on one box ((6, 5),
+// (6, 6) and 4-chunk x blocks in between); the hero kept (5, 5): 6.40-6.41
+// against 6.46-6.54 for each of those.
+constexpr int kLprHgFirst = 4;
+constexpr int kLprHgAhead = 4;
 
 // HG (half-groups, G = 32): lanes 0..31 and 32..63 of every wave take the 32
 // rows of two different groups, each lane still one row, all 64 tables in
@@ -114,8 +121,9 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   // it only when the wave's chunk count is NCH): kLprFirst / kLprAhead, one
   // straight-line sequence.
   constexpr int XB = NCH > 0 ? kLprXBlock : (NT == 1 && NB == 1) ? 4 : 2;
-  constexpr int R = NCH == 0 ? XB : (NCH < kLprFirst ? NCH : kLprFirst);
-  constexpr int DR = NCH == 0 ? XB : (R < kLprAhead ? R : kLprAhead);
+  constexpr int FIRST = HG ? kLprHgFirst : kLprFirst, AHEAD = HG ? kLprHgAhead : kLprAhead;
+  constexpr int R = NCH == 0 ? XB : (NCH < FIRST ? NCH : FIRST);
+  constexpr int DR = NCH == 0 ? XB : (R < AHEAD ? R : AHEAD);
   constexpr int LO = 16 / S;  // low nibbles of the table entries a thread builds
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
   typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
