@@ -371,6 +371,13 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr_hg(const uint8_t* w, const 
 // 12.14; without the nontemporal hint on the index loads 13.57.
 constexpr int kLpr8First = 5;
 constexpr int kLpr8Ahead = 5;
+// Passes of 4 or more vectors (each chunk's lookups feed 4+ products per
+// element, and x takes 8 SGPRs per chunk and vector) prefer a shallower
+// ring: config 4 at 4 vectors 13.25 against 13.87-13.91 us with (5, 5) on
+// one box, 13.76-13.86 against 14.15-14.24 on another ((2, 2), (3, 2), (4, 3),
+// (4, 4), (6, 6) and (8, 8) in between or slower); 1 and 2 vectors keep (5, 5).
+constexpr int kLpr8FirstWide = 3;
+constexpr int kLpr8AheadWide = 3;
 
 // 8-bit lane-per-row GEMV over GI weights (8-bit GI: [G x 512 B LUTs][K/16
 // chunks][G rows][16 B]; a chunk holds 16 elements).  The work layout of
@@ -397,8 +404,9 @@ __device__ __forceinline__ void lpr8_body(const LprArgs& a) {
   static_assert(EPI == kLprPlain || (NM == 2 && NB == 1), "gate/up epilogues are single-vector");
   constexpr int XB = NB >= 4 ? 1 : 2;  // x chunks per scalar block (8 SGPRs per chunk and vector)
   constexpr int LB = 4;                // NCH = 0: chunks per loop trip (ring slots)
-  constexpr int R = NCH == 0 ? LB : (NCH < kLpr8First ? NCH : kLpr8First);
-  constexpr int DR = NCH == 0 ? LB : (R < kLpr8Ahead ? R : kLpr8Ahead);
+  constexpr int F8 = NB >= 4 ? kLpr8FirstWide : kLpr8First, A8 = NB >= 4 ? kLpr8AheadWide : kLpr8Ahead;
+  constexpr int R = NCH == 0 ? LB : (NCH < F8 ? NCH : F8);
+  constexpr int DR = NCH == 0 ? LB : (R < A8 ? R : A8);
   constexpr int EPW = 256 / S;   // table entries each wave builds
   constexpr int LL = EPW / 8;    // 16-byte LUT loads per lane and matrix
   static_assert(NCH == 0 || NCH % XB == 0, "whole x blocks");
