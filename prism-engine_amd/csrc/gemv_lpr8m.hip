@@ -55,8 +55,13 @@ __device__ __forceinline__ void lpr8m_body(const LprArgs& a) {
   typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
   typedef float f32x16 __attribute__((ext_vector_type(16)));
   typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-  __shared__ uint32_t lds[kLprTableDw];
-  __shared__ __attribute__((aligned(16))) uint32_t xs[kLpr8mXDw];  // x, then the partials
+  // one static array with the lookup table first: the table's LDS address
+  // is 0, so a lookup's v_perm-built address is its ds_read address (with the
+  // table behind x, at 66 KB, past ds_read's 16-bit immediate offset, every
+  // lookup took one more v_add)
+  __shared__ __attribute__((aligned(16))) uint32_t lds_all[kLprTableDw + kLpr8mXDw];
+  uint32_t* const lds = lds_all;
+  uint32_t* const xs = lds_all + kLprTableDw;  // x, then the partials
   float* red = reinterpret_cast<float*>(xs);  // [Q][2 tiles][32 vectors][33]
 
   const uint32_t tid = threadIdx.x, lane = tid & 63;
@@ -126,18 +131,16 @@ __device__ __forceinline__ void lpr8m_body(const LprArgs& a) {
 
   const uint32_t lanebase = lane * 4u;
   const uint32_t psel = t ? 0x07060302u : 0x05040100u;  // this tile's halves of two dwords
-  const bool xlive = r32 < nb;
-  const uint32_t xoff = r32 * xrow + 8u * (c0 + h);  // dwords: vector r32, chunk c0 + h
+  // dwords: vector r32, chunk c0 + h.  Lanes of vectors past nb read vector
+  // nb - 1 instead of skipping the read: their B column only feeds output
+  // column r32, which is never stored (no branch, no zeroed operand per step)
+  const uint32_t xoff = (r32 < nb ? r32 : nb - 1) * xrow + 8u * (c0 + h);
   f32x16 acc;
 #pragma unroll
   for (int e = 0; e < 16; e++) acc[e] = 0.0f;
   auto step = [&](uint32_t s, int slot) {
-    u32x4v xb[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-    if (xlive) {
-      const u32x4v* xp = reinterpret_cast<const u32x4v*>(&xs[xoff + s * 16u]);
-      xb[0] = xp[0];
-      xb[1] = xp[1];
-    }
+    const u32x4v* xp = reinterpret_cast<const u32x4v*>(&xs[xoff + s * 16u]);
+    const u32x4v xb[2] = {xp[0], xp[1]};
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       uint32_t v[8];
