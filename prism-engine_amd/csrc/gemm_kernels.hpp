@@ -654,6 +654,46 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
 
   // ---- epilogue: D lane layout: col j = lane%32, row 8*(e/4) + 4*(lane/32) + e%4
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
+  if (full) {
+    // every element in range: buffer stores with the lane's column and
+    // half-row in the VGPR offset and the element's row within the tile (a
+    // compile-time multiple of N) in the scalar offset, so a store costs one
+    // scalar multiply, no per-element address arithmetic or exec-mask branch
+    // (the range check only sees the VGPR offset, which stays below 2^31)
+    const uint32_t lane_off = 4u * h * N + n0 + 64u * wave + j;  // elements from row m0
+    if constexpr (SPLIT) {
+      const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(P + (size_t)blockIdx.y * M * N + (size_t)m0 * N), (short)0, -1, kBufferWord3);
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const uint32_t so = (uint32_t)(32 * i + 8 * (e >> 2) + (e & 3)) * N * 4u;  // both columns' stores share it
+#pragma unroll
+          for (int s = 0; s < 2; s++) {
+            // the element is copied out first: a bit cast applied to the
+            // vector-element lvalue itself reads element 0 (hipcc 7.2)
+            const float v = acc[i][s][e];
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rp,
+                                                  (lane_off + 32u * s) * 4u, so, 0);
+          }
+        }
+    } else {
+      const __amdgpu_buffer_rsrc_t ry =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(Y + (size_t)m0 * N), (short)0, -1, kBufferWord3);
+#pragma unroll
+      for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const uint32_t so = (uint32_t)(32 * i + 8 * (e >> 2) + (e & 3)) * N * 2u;  // both columns' stores share it
+#pragma unroll
+          for (int s = 0; s < 2; s++)
+            __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (_Float16)acc[i][s][e]), ry,
+                                                  (lane_off + 32u * s) * 2u, so, 0);
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < 2; s++) {
     const uint32_t n = n0 + 64 * wave + 32 * s + j;
@@ -664,7 +704,7 @@ __global__ __launch_bounds__(256) void k_gemm_w4(const uint8_t* __restrict__ lut
 #pragma unroll
       for (int e = 0; e < 16; e++) {
         const uint32_t m = m0 + 32 * i + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (full || (m < M && n < N)) {
+        if (m < M && n < N) {
           if constexpr (SPLIT)
             pc[(size_t)m * N] = acc[i][s][e];
           else
