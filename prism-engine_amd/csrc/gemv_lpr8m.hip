@@ -13,8 +13,8 @@
 
 namespace prism {
 
-// 8-bit lane-per-row lookups feeding the matrix cores: the GEMV of 5..8
-// vectors over 8-bit GI weights (config 4 at batch 8), one workgroup of
+// 8-bit lane-per-row lookups feeding the matrix cores: the GEMV of 3..8
+// vectors over 8-bit GI weights (config 4 at batch 4 and 8), one workgroup of
 // 8 waves per group.  The lookups stay lane-private as in k_gemv_lpr8; the
 // products go to v_mfma_f32_32x32x16_f16, whose A operand is 32 weight rows
 // x 16 k (lane l: row l % 32, k 8 (l / 32) .. + 7) and whose B operand is up
@@ -35,7 +35,7 @@ namespace prism {
 //    halves, identically for weights and x, so the products are the same.
 //  * x (nb * K halves, at most 64 KB) is copied to LDS once per workgroup,
 //    each vector followed by 16 bytes of padding so that the lanes r < nb,
-//    which read their vector's 16 bytes per MFMA (the others pass zeros),
+//    which read their vector's 16 bytes per MFMA (the others read nothing),
 //    fall in distinct bank groups (unpadded, vectors K * 2 bytes apart all
 //    start in bank 0: bank-conflict cycles exceeded the LDS-active cycles at
 //    8 vectors).  The LDS then holds the four quarters' fp32 partials, added
@@ -44,11 +44,13 @@ namespace prism {
 // Per 32 elements of a row: 32 lookups, 48 VALU ops, 2 MFMAs.  Requires
 // K % 512 == 0, nb <= 32, nb * (K / 2 + kLpr8mXPad) <= kLpr8mXDw, 16-byte
 // aligned x and the weight block below 2 GiB.  Config 4 (14336 x 4096, 56-row groups), MI355X,
-// both kernels in one run: 8 vectors 15.0-15.2 us against 17.9-18.2 for
-// k_gemv_lpr8; 2 / 3 / 4 vectors 14.1-14.4 / 14.2-14.3 / 14.3-14.4 against
-// 12.1 / 13.5-13.6 / 13.5-13.8, so up to 4 stay with k_gemv_lpr8.  With x
-// read from global memory per MFMA 17.7 / 18.1 us at 4 / 8; 2 or 8 double
-// steps ahead, or two accumulators, no faster.
+// both kernels in one run, before the lanes past nb stopped reading x:
+// 8 vectors 15.0-15.2 us against 17.9-18.2 for k_gemv_lpr8; 2 / 3 / 4
+// vectors 14.1-14.4 / 14.2-14.3 / 14.3-14.4 against 12.1 / 13.5-13.6 /
+// 13.5-13.8.  With those reads gone it also takes 3 and 4 vectors (the
+// dispatch in prism_hip.hip has the numbers).  With x read from global
+// memory per MFMA 17.7 / 18.1 us at 4 / 8; 2 or 8 double steps ahead, or
+// two accumulators, no faster.
 __device__ __forceinline__ void lpr8m_body(const LprArgs& a) {
   constexpr int Q = 4;  // K quarters
   constexpr int AH = kLpr8mAhead;
@@ -131,16 +133,26 @@ __device__ __forceinline__ void lpr8m_body(const LprArgs& a) {
 
   const uint32_t lanebase = lane * 4u;
   const uint32_t psel = t ? 0x07060302u : 0x05040100u;  // this tile's halves of two dwords
-  // dwords: vector r32, chunk c0 + h.  Lanes of vectors past nb read vector
-  // nb - 1 instead of skipping the read: their B column only feeds output
-  // column r32, which is never stored (no branch, no zeroed operand per step)
+  // dwords: vector r32, chunk c0 + h (lanes of vectors past nb skip their
+  // reads below; their offset stays inside x all the same)
   const uint32_t xoff = (r32 < nb ? r32 : nb - 1) * xrow + 8u * (c0 + h);
   f32x16 acc;
 #pragma unroll
   for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+  // Only the lanes of real vectors read x: the others' B columns keep stale
+  // values, which reach only the output columns r32 >= nb (never stored).
+  // LDS returns data for active lanes only, so at 8 vectors a step's x reads
+  // take 16 lanes' worth of LDS cycles instead of 64 (config 4 at 8 vectors
+  // 13.13-13.21 against 13.83-13.86 us, at 5 vectors 13.00-13.09 against
+  // 13.54-13.61, alternating on one box).
+  u32x4v xb[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  const bool xlive = r32 < nb;
   auto step = [&](uint32_t s, int slot) {
     const u32x4v* xp = reinterpret_cast<const u32x4v*>(&xs[xoff + s * 16u]);
-    const u32x4v xb[2] = {xp[0], xp[1]};
+    if (xlive) {
+      xb[0] = xp[0];
+      xb[1] = xp[1];
+    }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       uint32_t v[8];

@@ -786,13 +786,17 @@ int launch_lpr8(prism_hip_ctx* ctx, dim3 groups, hipStream_t st, const prism::Lp
 }
 
 // GEMV over 8-bit GI weights: gate + up (SwiGLU, or the pair with d_y2) in
-// one k_gemv_lpr8 pass; one matrix in passes of 1 / 2 / 4 vectors
-// (k_gemv_lpr8), of 5..8 with the lane-per-row lookups feeding the matrix
-// cores when x fits its LDS (k_gemv_lpr8m: nb * (K / 2 + 4) <= 16512), else of 8
-// (k_gemv_lpr8), or of up to 16 on the matrix cores from 9 vectors on
-// (from 5 when the chunk count is not a compile-time one and x does not fit
-// k_gemv_lpr8m) (k_gemv_mfma<8, GI>).  x not 16-byte aligned: the generic
-// kernel.
+// one k_gemv_lpr8 pass; one matrix in passes of 1 / 2 vectors (k_gemv_lpr8),
+// of 3..8 with the lane-per-row lookups feeding the matrix cores when x fits
+// their LDS (k_gemv_lpr8m: nb * (K / 2 + 4) <= 16512), else of 4 or 8
+// (k_gemv_lpr8; 3..4 vectors then have K > 8248, so the run-time chunk loop),
+// or of up to 16 on the matrix cores from 9 vectors on (from 5 when the
+// chunk count is not a compile-time one and x does not fit k_gemv_lpr8m)
+// (k_gemv_mfma<8, GI>).  x not 16-byte aligned: the generic kernel.
+// Config 4 (14336 x 4096), MI355X, alternating on one box: 3 / 4 vectors
+// 12.77-12.81 / 12.95-13.05 us on k_gemv_lpr8m against 13.37-13.50 /
+// 13.27-13.39 on k_gemv_lpr8; 2 vectors 12.73-12.80 against 11.92-11.96, so
+// 2 stay with k_gemv_lpr8.
 int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hip_weight* w2, const void* d_x,
                     uint32_t nb, void* d_y, void* d_y2, hipStream_t st) {
   const uint32_t N = w->dim_m, K = w->dim_n;
@@ -842,7 +846,7 @@ int launch_gemv_gi8(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_h
       ga.y = y;
       ga.nb = chunk = left;
       PRISM_LAUNCH((prism::k_gemv_generic<8, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, ga);
-    } else if (left >= 5 && left <= 8 && left * (K / 2 + prism::kLpr8mXPad) <= (uint32_t)prism::kLpr8mXDw) {
+    } else if (left >= 3 && left <= 8 && left * (K / 2 + prism::kLpr8mXPad) <= (uint32_t)prism::kLpr8mXDw) {
       prism::LprArgs a{};
       a.G = G;
       a.w = w->d;

@@ -299,9 +299,9 @@ GI8_SHAPES = [(14336, 4096), (9100, 2048), (8192, 2560), (16384, 2048)]
 @pytest.mark.parametrize("N,K", GI8_SHAPES)
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 20])
 def test_gi8_gemv(pe, oracle, gpu_ctx, N, K, batch):
-    """8-bit GI: k_gemv_lpr8 passes of 1 / 2 / 4 vectors, k_gemv_lpr8m for
-    5..8 (lookups into the matrix cores) and the matrix-core GEMV over GI from
-    9 vectors on."""
+    """8-bit GI: k_gemv_lpr8 passes of 1 / 2 vectors, k_gemv_lpr8m for 3..8
+    (lookups into the matrix cores) and the matrix-core GEMV over GI from 9
+    vectors on."""
     assert _gi(N, K, 8)
     if N * K > 4 * 10**7 and batch in (3, 5, 9):
         pytest.skip("odd batches covered at the smaller shapes")
@@ -349,8 +349,8 @@ def test_gi4_decode_bit_exact_through_lpr(pe, gpu_ctx, N, K):
 @pytest.mark.parametrize("N,K", [(14336, 4096), (8192, 2560)])
 def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     """One-hot x: every output is LUT_r[idx(r, k)] exactly, through the
-    8-bit lane-per-row GEMV at 1 and 4 vectors, its matrix-core form at 8 and
-    the matrix-core GEMV over GI (eleven vectors)."""
+    8-bit lane-per-row GEMV at 1 and 2 vectors, its matrix-core form at 4 and
+    8 and the matrix-core GEMV over GI (eleven vectors)."""
     t = pe.synth_tensor(N, K, 8, seed=K + 13)
     lut, idx = pe.unpack_payload(t.payload, N, K, 8)
     ks = [0, 1, 15, 16, 17, K // 2 + 5, K // 3, K - 17, K - 16, K - 2, K - 1]
@@ -360,6 +360,7 @@ def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     w = gpu_ctx.upload_tensor(t)
     print(f"gi8 one-hot {N}x{K}", flush=True)
     ys = gpu_ctx.gemv(w, x.view(np.uint16))
+    y2 = gpu_ctx.gemv(w, x[:2].view(np.uint16))
     y4 = gpu_ctx.gemv(w, x[:4].view(np.uint16))
     y8 = gpu_ctx.gemv(w, x[:8].view(np.uint16))
     for i, k in enumerate(ks):
@@ -368,8 +369,10 @@ def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
         y1 = gpu_ctx.gemv(w, x[i:i + 1].view(np.uint16))[0]
         assert np.array_equal(y1, want), f"column {k}, one vector"
         assert np.array_equal(ys[i], want), f"column {k}, eleven vectors"
+        if i < 2:
+            assert np.array_equal(y2[i], want), f"column {k}, two vectors"
         if i < 4:
-            assert np.array_equal(y4[i], want), f"column {k}, four vectors"
+            assert np.array_equal(y4[i], want), f"column {k}, four vectors (matrix cores fed by lookups)"
         if i < 8:
             assert np.array_equal(y8[i], want), f"column {k}, eight vectors (matrix cores fed by lookups)"
     w.free()
@@ -467,18 +470,37 @@ def test_gi8_gemm(pe, oracle, gpu_ctx, M):
 
 
 @pytest.mark.parametrize("batch,kernel", [(1, "k_gemv_lpr8<8, 1, 1, 0, 64>"), (2, "k_gemv_lpr8<8, 1, 2, 0, 64>"),
-                                          (4, "k_gemv_lpr8<8, 1, 4, 0, 64>"), (5, "k_gemv_lpr8<8, 1, 8, 0, 64>"),
-                                          (8, "k_gemv_lpr8<8, 1, 8, 0, 64>")])
+                                          (3, "k_gemv_lpr8m"), (4, "k_gemv_lpr8m"),
+                                          (5, "k_gemv_lpr8<8, 1, 8, 0, 64>"), (8, "k_gemv_lpr8<8, 1, 8, 0, 64>")])
 def test_gi8_gemv_k8192(pe, oracle, gpu_ctx, batch, kernel):
     """8-bit GI with K = 8192: each wave's 64 chunks as a compile-time
-    count.  1, 2 and 4 vectors a pass, and the 8-vector form for 5..8
-    (x of five 8192-element vectors, 5 x 4100 dwords, does not fit
-    k_gemv_lpr8m's 16512-dword LDS), against the oracle; the library's
-    launch report names the kernel that ran."""
+    count.  1 and 2 vectors a pass, k_gemv_lpr8m at 3 and 4 (4 x 4100
+    dwords of x fit its 16512-dword LDS), and the 8-vector form for 5..8
+    (x of five 8192-element vectors, 5 x 4100 dwords, does not fit),
+    against the oracle; the library's launch report names the kernel that
+    ran."""
     N, K = 14336, 8192
     assert _gi(N, K, 8)
     t = pe.synth_tensor(N, K, 8, seed=K + batch)
     x = pe.synth_x(batch, K, seed=batch + 81)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi8 gemv {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    assert gpu_ctx.last_kernels() == kernel
+    _check(y, oracle.gemv(x, t.payload, N, K, 8, threads=8), f"GI8 {N}x{K} batch {batch}")
+    w.free()
+
+
+@pytest.mark.parametrize("batch,kernel", [(3, "k_gemv_lpr8m"), (4, "k_gemv_lpr8<8, 1, 4, 0, 0>")])
+def test_gi8_wide_rows_three_four_vectors(pe, oracle, gpu_ctx, batch, kernel):
+    """3 and 4 vectors of 8704-element rows: 3 x 4356 dwords of x fit
+    k_gemv_lpr8m's LDS, 4 x 4356 do not, so 4 vectors take k_gemv_lpr8's
+    4-vector pass in its run-time chunk loop (68 chunks per wave), the only
+    shapes that reach that pass; against the oracle."""
+    N, K = 8192, 8704
+    assert _gi(N, K, 8)
+    t = pe.synth_tensor(N, K, 8, seed=K + batch)
+    x = pe.synth_x(batch, K, seed=batch + 87)
     w = gpu_ctx.upload_tensor(t)
     print(f"gi8 gemv {N}x{K} batch {batch}", flush=True)
     y = gpu_ctx.gemv(w, x)
