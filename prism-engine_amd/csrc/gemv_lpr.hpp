@@ -558,10 +558,12 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr8(const uint8_t* w, const ui
   lpr8_body<S, NM, NB, EPI, NCH>(lpr_args(w, w2, x, y, y2, N, K, nb, G));
 }
 
-// k_gemv_lpr8m, the 8-bit GEMV of 5..8 vectors with these lookups feeding
-// the matrix cores, is built in its own translation unit (gemv_lpr8m.hip)
-// with the max-ilp machine scheduler; this launches it on `st`.
+// k_gemv_lpr8m and k_gemv_lpr4m, the 8- and 4-bit GEMVs of 3..8 vectors
+// with these lookups feeding the matrix cores, are built in their own
+// translation unit (gemv_lpr8m.hip) with the max-ilp machine scheduler;
+// these launch them on `st`.
 hipError_t launch_gemv_lpr8m(dim3 groups, hipStream_t st, const LprArgs& a);
+hipError_t launch_gemv_lpr4m(dim3 groups, hipStream_t st, const LprArgs& a);
 
 // Split-block payload (LUT block then index rows) -> GI with G rows per
 // group, 4- or 8-bit.  One thread per 16-byte piece of the GI block, in GI

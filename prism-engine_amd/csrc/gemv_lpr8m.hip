@@ -1,6 +1,8 @@
-// gemv_lpr8m.hip -- k_gemv_lpr8m, built in its own translation unit with
-// the max-ilp machine scheduler (-mllvm -amdgpu-sched-strategy=max-ilp in
-// the Makefile).  That schedule suits only this kernel: config 4 at 8
+// gemv_lpr8m.hip -- k_gemv_lpr8m and k_gemv_lpr4m (lane-per-row lookups
+// feeding the matrix cores, 8- and 4-bit), built in their own translation
+// unit with the max-ilp machine scheduler (-mllvm
+// -amdgpu-sched-strategy=max-ilp in the Makefile).  That schedule suits
+// only these kernels: config 4 at 8
 // vectors 14.50-14.61 against 15.32-15.38 us with the default scheduler,
 // while the same flag on the whole library slowed the hero GEMV (6.63-6.68
 // against 6.49-6.57 us), config 4 at 4 vectors (14.8 against 13.6), cfg2,
@@ -193,6 +195,159 @@ __device__ __forceinline__ void lpr8m_body(const LprArgs& a) {
     const uint32_t grow = g * G + r;
     if (r < G && grow < N) a.y[(size_t)b * N + grow] = f2h(sum);
   }
+}
+
+// The 4-bit form: the same waves (tile t = w & 1, K quarter q = w >> 1),
+// x in LDS read by the lanes of live vectors only, one accumulator of
+// v_mfma_f32_32x32x16_f16 per wave; the table is the 4-bit lane-per-row
+// pair table (entry b = LUT[b & 15] | LUT[b >> 4] << 16, the fp16 pair of
+// an index byte, at LDS dword 64 b + row), so one lookup gives two
+// consecutive k of the A operand and four lookups (one index dword) are a
+// whole MFMA operand, with no packing.  The two lanes of a row (h = 0, 1)
+// read the same bank.  A double step covers two 32-element chunks: lane
+// (r, h) takes chunk 2 s + h of its quarter for row 32 t + r; MFMA j of the
+// step takes index dword j of that chunk (elements 8 j .. 8 j + 7) and x[r]
+// at the same k.  Requires K % 256 == 0.
+__device__ __forceinline__ void lpr4m_body(const LprArgs& a) {
+  constexpr int Q = 4;
+  constexpr int AH = kLpr8mAhead;
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  __shared__ __attribute__((aligned(16))) uint32_t lds_all[kLprTableDw + kLpr8mXDw];
+  uint32_t* const lds = lds_all;
+  uint32_t* const xs = lds_all + kLprTableDw;
+  float* red = reinterpret_cast<float*>(xs);  // [Q][2 tiles][32 vectors][33]
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t t = w & 1, q = w >> 1;
+  const uint32_t g = blockIdx.x;
+  const uint32_t N = a.N, K = a.K, G = a.G, nb = a.nb;
+  const uint32_t r32 = lane & 31, h = lane >> 5;
+  const uint32_t gbytes = gi_group_bytes(G, K, 4);
+  const uint32_t gbase = g * gbytes;
+  const __amdgpu_buffer_rsrc_t ri =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)(gridDim.x * gbytes), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(nb * K * 2u), kBufferWord3);
+
+  // ---- the LUT of row `lane` (every wave builds 1/8 of every row's table),
+  // x, and the first index chunks
+  uint32_t L[8];
+  {
+    const uint32_t lo = lane < G ? gbase + lane * 32u : 0x80000000u;
+    const u32x4v l0 = __builtin_amdgcn_raw_buffer_load_b128(ri, lo, 0u, 0);
+    const u32x4v l1 = __builtin_amdgcn_raw_buffer_load_b128(ri, lo + 16u, 0u, 0);
+    L[0] = l0.x; L[1] = l0.y; L[2] = l0.z; L[3] = l0.w;
+    L[4] = l1.x; L[5] = l1.y; L[6] = l1.z; L[7] = l1.w;
+  }
+  const uint32_t xq = nb * K / 8;
+  u32x4v xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t p = tid + 512u * i;
+    xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, p < xq ? p * 16u : 0x80000000u, 0u, 0);
+  }
+  const uint32_t nc = K / 32;              // chunks per row
+  const uint32_t nd = nc / (Q * 2);        // double steps per wave
+  const uint32_t c0 = q * (nc / Q);
+  const uint32_t row = 32 * t + r32;
+  const uint32_t ibase = row < G ? gbase + G * 32u + ((c0 + h) * G + row) * kGiChunk : 0x80000000u;
+  const uint32_t istep = 2u * G * kGiChunk;  // two chunks of the group
+  u32x4v ir[AH];
+  auto ld = [&](uint32_t s, int slot) {
+    ir[slot] = __builtin_amdgcn_raw_buffer_load_b128(ri, s < nd ? ibase + s * istep : 0x80000000u, 0u, kNontemporal);
+  };
+#pragma unroll
+  for (int u = 0; u < AH; u++) ld(u, u);
+
+  const uint32_t xrow = K / 2 + kLpr8mXPad;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t p = tid + 512u * i;
+    if (p < xq) {
+      const uint32_t b = p / (K / 8), o = p % (K / 8);
+      *reinterpret_cast<u32x4v*>(&xs[b * xrow + 4 * o]) = xv[i];
+    }
+  }
+  // entries e = w + 8 i: low nibble w + 8 (i % 2) (from the LUT registers
+  // with the wave-uniform w), high nibble i / 2
+  uint32_t hv[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const uint32_t e = w + 8u * j;
+    uint32_t d = L[0];
+#pragma unroll
+    for (int k = 1; k < 8; k++) d = (e >> 1) == (uint32_t)k ? L[k] : d;
+    hv[j] = (e & 1) ? (d >> 16) : (d & 0xFFFFu);
+  }
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    const int hi = i / 2;
+    lds[(w + 8 * i) * 64 + lane] = __builtin_amdgcn_perm(L[hi >> 1], hv[i % 2], (hi & 1) ? 0x07060100u : 0x05040100u);
+  }
+  __syncthreads();
+
+  const uint32_t rowbase = row * 4u;  // byte 0 of a lookup address: the row's bank
+  const uint32_t xoff = (r32 < nb ? r32 : nb - 1) * xrow + 16u * (c0 + h);
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+  u32x4v xb[4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+  const bool xlive = r32 < nb;
+  auto step = [&](uint32_t s, int slot) {
+    const u32x4v* xp = reinterpret_cast<const u32x4v*>(&xs[xoff + s * 32u]);
+    if (xlive) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) xb[j] = xp[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t wd = ir[slot][j];
+      u32x4v A;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t ad = __builtin_amdgcn_perm(wd, rowbase, 0x0C0C0000u | ((4u + i) << 8));
+        A[i] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds) + ad);
+      }
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, A), __builtin_bit_cast(f16x8, xb[j]), acc,
+                                                   0, 0, 0);
+    }
+  };
+  for (uint32_t s = 0; s < nd; s += AH) {
+#pragma unroll
+    for (int u = 0; u < AH; u++) {
+      if (s + u < nd) step(s + u, u);
+      ld(s + u + AH, u);
+    }
+  }
+
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 16; e++) red[((q * 2 + t) * 32 + r32) * 33 + 8 * (e >> 2) + 4 * h + (e & 3)] = acc[e];
+  __syncthreads();
+  for (uint32_t i = tid; i < 64u * nb; i += 512) {
+    const uint32_t b = i / 64, r = i % 64;
+    const uint32_t tt = r / 32, rr = r % 32;
+    float sum = red[(tt * 32 + b) * 33 + rr];
+#pragma unroll
+    for (int v = 1; v < Q; v++) sum += red[((v * 2 + tt) * 32 + b) * 33 + rr];
+    const uint32_t grow = g * G + r;
+    if (r < G && grow < N) a.y[(size_t)b * N + grow] = f2h(sum);
+  }
+}
+
+__global__ __launch_bounds__(512) void k_gemv_lpr4m(const uint8_t* w, const uint8_t* w2, const uint16_t* x,
+                                                     uint16_t* y, uint16_t* y2, uint32_t N, uint32_t K, uint32_t nb,
+                                                     uint32_t G) {
+  lpr4m_body(lpr_args(w, w2, x, y, y2, N, K, nb, G));
+}
+
+hipError_t launch_gemv_lpr4m(dim3 groups, hipStream_t st, const LprArgs& a) {
+  note_launch(reinterpret_cast<const void*>(&k_gemv_lpr4m));
+  hipLaunchKernelGGL(k_gemv_lpr4m, groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
+  return hipGetLastError();
 }
 
 __global__ __launch_bounds__(512) void k_gemv_lpr8m(const uint8_t* w, const uint8_t* w2, const uint16_t* x,

@@ -722,9 +722,11 @@ int launch_gemv_raw(prism_hip_ctx* ctx, uint32_t bits, uint32_t N, uint32_t K, c
 }
 
 // GEMV over GI weights (w2: gate + up, SwiGLU or with d_y2 the pair).
-// One or two vectors a pass: k_gemv_lpr; three or more: the matrix-core
-// kernel (K % 128 == 0) in passes of up to 16, else lane-per-row passes of
-// two.  x not 16-byte aligned: the generic kernel.
+// One or two vectors a pass: k_gemv_lpr; three to eight over groups of more
+// than 32 rows, K % 256 == 0 and x within its LDS: k_gemv_lpr4m; otherwise
+// three or more: the matrix-core kernel (K % 128 == 0) in passes of up to
+// 16, else lane-per-row passes of two.  x not 16-byte aligned: the generic
+// kernel.
 // k_gemv_lpr with the wave's chunk count as a compile-time constant when
 // every wave has the same count (K/32 a multiple of S) and it is 8 or 16,
 // else the run-time loop.
@@ -948,6 +950,23 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.K = K;
       a.nb = chunk = left;
       PRISM_LAUNCH((prism::k_gemv_generic<4, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, a);
+    } else if (!hg && G > 32 && left >= 3 && left <= 8 && K % 256 == 0 &&
+               left * (K / 2 + prism::kLpr8mXPad) <= (uint32_t)prism::kLpr8mXDw) {
+      // 3..8 vectors over groups of 33..64 rows (both row tiles of
+      // k_gemv_lpr4m busy) when x fits its LDS.  MI355X, 14336 x 4096,
+      // alternating on one box: 3 / 4 / 8 vectors 8.16-8.24 / 8.26-8.29 /
+      // 9.02 us against 9.40-9.42 / 9.48-9.51 / 10.07-10.22 for
+      // k_gemv_mfma<4, GI>; 1 / 2 vectors 7.97 / 8.07-8.13 against
+      // 6.36-6.38 / 7.59-7.91 for k_gemv_lpr, which keeps them.
+      prism::LprArgs a{};
+      a.G = G;
+      a.w = w->d;
+      a.x = x;
+      a.y = y;
+      a.N = N;
+      a.K = K;
+      a.nb = chunk = left;
+      HIP_TRY(ctx, prism::launch_gemv_lpr4m(groups, st, a));
     } else if (left >= 3 && K % prism::kGmGroup == 0) {
       prism::GemvArgs a{};
       a.gi = G;

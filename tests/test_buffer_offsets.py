@@ -408,3 +408,71 @@ def test_gemv_lpr8m_offsets(N, K, nb):
     assert dst.max() + 4 <= LPR8M_XDW and len(np.unique(dst)) == xq
     # partials: [Q][2][32][33] floats in the x region
     assert (Q * 2 * 32 + 31) * 33 + 31 < LPR8M_XDW
+
+
+@pytest.mark.parametrize("N,K,nb", [(14336, 4096, 8), (14336, 4096, 3), (9100, 2048, 8), (16384, 2048, 5),
+                                    (14336, 8192, 4), (9000, 2304, 7), (12000, 3328, 6)])
+def test_gemv_lpr4m_offsets(N, K, nb):
+    """k_gemv_lpr4m (gemv_lpr8m.hip): the LUT of row `lane` (two 16-byte
+    loads, rows past G an offset past the range); x in 16-byte pieces; double
+    step s's chunk c0 + 2s + h of row 32t + r, or an offset past the range
+    from nd on (the loop requests AH past its last step, in whole blocks of
+    AH even when AH does not divide nd); the x reads' LDS dwords, the table's
+    and the lookups' LDS indices."""
+    G = gi_rows(N, K)
+    xrow = K // 2 + LPR8M_XPAD
+    assert G > 32 and K % 256 == 0 and 3 <= nb <= 8 and nb * xrow <= LPR8M_XDW, "the host's condition"
+    Q, AH = 4, LPR8M_AHEAD
+    nc = K // 32
+    nd = nc // (Q * 2)
+    lane = np.arange(64)
+    r32, h = lane % 32, lane // 32
+    ngroups = -(-N // G)
+    gb = gi_group_bytes(G, K)
+    nbytes = ngroups * gb
+    for g in (0, ngroups - 1):
+        base = g * gb
+        lo = np.where(lane < G, base + lane * 32, 0x80000000)
+        for i in range(2):
+            perf = _check(lo + 16 * i, 0, 16, nbytes, nbytes, "gemv_lpr4m LUT")
+            assert (perf == (lane < G)).all()
+            assert ((lo + 16 * i + 16) <= base + G * 32)[perf].all(), "LUT load leaves the group's LUTs"
+        for w in range(8):
+            t, q = w & 1, w >> 1
+            row = 32 * t + r32
+            c0 = q * (nc // Q)
+            ibase = np.where(row < G, base + G * 32 + ((c0 + h) * G + row) * GI_CHUNK, 0x80000000)
+            steps = -(-nd // AH) * AH + AH  # every ld() the loop issues
+            for s in range(steps):
+                io = ibase + s * 2 * G * GI_CHUNK if s < nd else np.full(64, 0x80000000)
+                perf = _check(io, 0, 16, nbytes, nbytes, "gemv_lpr4m chunk")
+                assert (perf == ((row < G) & (s < nd))).all()
+                assert ((io + 16) <= base + gb)[perf].all(), "chunk load leaves its group"
+                assert (c0 + 2 * s + h < c0 + nc // Q)[perf].all(), "chunk outside the wave's K quarter"
+            # x from LDS: lanes r < nb read dwords xoff + 32 s + 4 j .. + 3, j < 4
+            xoff = r32 * xrow + 16 * (c0 + h)
+            live = r32 < nb
+            last = xoff + 32 * (nd - 1) + 16
+            assert (last[live] <= r32[live] * xrow + K // 2).all()
+            for s in (0, nd - 1):
+                for j in range(4):
+                    xel = 2 * (xoff + 32 * s + 4 * j - r32 * xrow)
+                    wel = 32 * (c0 + 2 * s + h) + 8 * j
+                    assert (xel == wel).all(), "x and weight elements of an MFMA differ"
+            for grp in range(4):
+                ln = np.arange(16 * grp, 16 * grp + 16)
+                ln = ln[r32[ln] < nb]
+                banks = (xoff[ln] % 64) // 4
+                assert len(set(banks.tolist())) == len(ln), "x reads conflict"
+    # the table: wave w writes entries w + 8i of every row at dword 64 e + row;
+    # a lookup of index byte b for row 32t + r reads dword 64 b + row
+    e = (np.arange(8)[:, None] + 8 * np.arange(32)[None, :]).ravel()
+    assert sorted(e.tolist()) == list(range(256)), "the waves build every entry once"
+    assert (e.max() * 64 + 63) < 256 * 64 and 255 * 64 + 63 < 256 * 64
+    tid = np.arange(512)
+    xq = nb * K // 8
+    for i in range(8):
+        p = tid + 512 * i
+        perf = _check(np.where(p < xq, p * 16, 0x80000000), 0, 16, nb * K * 2, nb * K * 2, "gemv_lpr4m x")
+        assert (perf == (p < xq)).all()
+    assert ((tid[:, None] + 512 * np.arange(8)[None, :]) < xq).sum() == xq, "x pieces cover x once"

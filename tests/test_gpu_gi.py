@@ -56,7 +56,7 @@ def _gi(N, K, bits=4, num_cu=256):
 
 
 @pytest.mark.parametrize("N,K", GI_SHAPES)
-@pytest.mark.parametrize("batch", [1, 2, 3, 5, 16])
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 8, 16])
 def test_gi_gemv(pe, oracle, gpu_ctx, N, K, batch):
     assert _gi(N, K)
     if N * K > 4 * 10**7 and batch in (3, 5):
@@ -346,6 +346,71 @@ def test_gi4_decode_bit_exact_through_lpr(pe, gpu_ctx, N, K):
     w.free()
 
 
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
+def test_gi4_decode_bit_exact_through_lpr4m(pe, gpu_ctx, N, K):
+    """One-hot x, a different column per vector, through the 4-bit
+    lane-per-row lookups feeding the matrix cores (k_gemv_lpr4m, 3 and 8
+    vectors): every output is LUT_r[idx(r, k)] exactly.  The columns cover
+    both lanes of a row (chunks 2s and 2s + 1), every MFMA of a step (index
+    dwords 0..3 of a chunk), the K quarters' edges and the row's end."""
+    t = pe.synth_tensor(N, K, 4, seed=K + 41)
+    lut, idx = pe.unpack_payload(t.payload, N, K, 4)
+    q = K // 4
+    ks = [0, 1, 7, 8, 31, 32, 33, 63, 64 + 17, q - 1, q, K // 2 + 5, K - 33, K - 32, K - 9, K - 1]
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi4 one-hot lpr4m {N}x{K}", flush=True)
+    rows = np.arange(N)
+    for nb in (3, 8):
+        for c0 in range(0, len(ks), nb):
+            cols = ks[c0:c0 + nb]
+            if len(cols) < 3:
+                continue
+            x = np.zeros((len(cols), K), dtype=np.float16)
+            for v, k in enumerate(cols):
+                x[v, k] = 1.0
+            y = gpu_ctx.gemv(w, x.view(np.uint16))
+            assert gpu_ctx.last_kernels() == "k_gemv_lpr4m"
+            for v, k in enumerate(cols):
+                want = lut[rows, idx[:, k]]
+                want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
+                bad = np.nonzero(y[v] != want)[0]
+                assert bad.size == 0, f"column {k}, {len(cols)} vectors: {bad.size} rows differ"
+    w.free()
+
+
+@pytest.mark.parametrize("batch,kernel", [(3, "k_gemv_lpr4m"), (4, "k_gemv_lpr4m"), (5, "k_gemv_mfma<4, true>")])
+def test_gi4_k8192_lpr4m_edge(pe, oracle, gpu_ctx, batch, kernel):
+    """4-bit GI rows of 8192 (32 double steps per wave): 3 and 4 vectors of
+    x (4 x 4100 dwords) fit k_gemv_lpr4m's LDS, 5 do not and take the
+    matrix-core GEMV; against the oracle."""
+    N, K = 14336, 8192
+    assert _gi(N, K) == 56
+    t = pe.synth_tensor(N, K, 4, seed=K + batch + 4)
+    x = pe.synth_x(batch, K, seed=batch + 44)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi4 gemv {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    assert gpu_ctx.last_kernels() == kernel
+    _check(y, oracle.gemv(x, t.payload, N, K, 4, threads=8), f"GI4 {N}x{K} batch {batch}")
+    w.free()
+
+
+@pytest.mark.parametrize("N,K,batch", [(9000, 2304, 5), (12000, 3328, 7), (16384, 2048, 4)])
+def test_gi4_lpr4m_row_lengths(pe, oracle, gpu_ctx, N, K, batch):
+    """k_gemv_lpr4m where a wave's double steps are not a multiple of the
+    four in flight (K = 2304: 9 per wave; 3328: 13), and over 64-row groups;
+    against the oracle."""
+    assert _gi(N, K) > 32
+    t = pe.synth_tensor(N, K, 4, seed=N + K + batch)
+    x = pe.synth_x(batch, K, seed=batch + 61)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi4 lpr4m {N}x{K} batch {batch}", flush=True)
+    y = gpu_ctx.gemv(w, x)
+    assert gpu_ctx.last_kernels() == "k_gemv_lpr4m"
+    _check(y, oracle.gemv(x, t.payload, N, K, 4, threads=8), f"GI4 {N}x{K} batch {batch}")
+    w.free()
+
+
 @pytest.mark.parametrize("N,K", [(14336, 4096), (8192, 2560)])
 def test_gi8_decode_bit_exact_through_gemv(pe, gpu_ctx, N, K):
     """One-hot x: every output is LUT_r[idx(r, k)] exactly, through the
@@ -541,8 +606,8 @@ def test_last_kernels_reports_the_dispatch(pe, gpu_ctx):
     assert gpu_ctx.last_kernels() == "k_gemv_lpr<8, 1, 1, 0, 16>"
     gpu_ctx.gemv(w, pe.synth_x(2, K, seed=1))
     assert gpu_ctx.last_kernels() == "k_gemv_lpr<8, 1, 2, 0, 16>"
-    gpu_ctx.gemv(w, pe.synth_x(40, K, seed=1))  # 16 + 16 + 8 vectors on the matrix cores
-    assert gpu_ctx.last_kernels() == "k_gemv_mfma<4, true> x3"
+    gpu_ctx.gemv(w, pe.synth_x(40, K, seed=1))  # 16 + 16 on the matrix-core GEMV, 8 on k_gemv_lpr4m
+    assert gpu_ctx.last_kernels() == "k_gemv_mfma<4, true> x2 + k_gemv_lpr4m"
     small = gpu_ctx.upload_tensor(pe.synth_tensor(4864, 896, 4, seed=6))
     gpu_ctx.gemv(small, pe.synth_x(1, 896, seed=1))
     assert gpu_ctx.last_kernels().startswith("k_gemv_tile<")
