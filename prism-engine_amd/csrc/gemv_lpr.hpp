@@ -559,11 +559,14 @@ __global__ __launch_bounds__(64 * S) void k_gemv_lpr8(const uint8_t* w, const ui
 }
 
 // k_gemv_lpr8m and k_gemv_lpr4m, the 8- and 4-bit GEMVs of 3..8 vectors
-// with these lookups feeding the matrix cores, are built in their own
+// with these lookups feeding the matrix cores (and k_gemv_lpr4q), are built in their own
 // translation unit (gemv_lpr8m.hip) with the max-ilp machine scheduler;
 // these launch them on `st`.
 hipError_t launch_gemv_lpr8m(dim3 groups, hipStream_t st, const LprArgs& a);
 hipError_t launch_gemv_lpr4m(dim3 groups, hipStream_t st, const LprArgs& a);
+// k_gemv_lpr4q (the same unit): the 4-bit GEMV of 3..4 vectors with the
+// products on the matrix cores' 4 x 4 x 4 blocks.
+hipError_t launch_gemv_lpr4q(dim3 groups, hipStream_t st, const LprArgs& a);
 
 // Split-block payload (LUT block then index rows) -> GI with G rows per
 // group, 4- or 8-bit.  One thread per 16-byte piece of the GI block, in GI

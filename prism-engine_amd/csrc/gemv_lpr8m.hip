@@ -1,5 +1,5 @@
-// gemv_lpr8m.hip -- k_gemv_lpr8m and k_gemv_lpr4m (lane-per-row lookups
-// feeding the matrix cores, 8- and 4-bit), built in their own translation
+// gemv_lpr8m.hip -- k_gemv_lpr8m, k_gemv_lpr4m and k_gemv_lpr4q (lane-per-row
+// lookups feeding the matrix cores, 8- and 4-bit), built in their own translation
 // unit with the max-ilp machine scheduler (-mllvm
 // -amdgpu-sched-strategy=max-ilp in the Makefile).  That schedule suits
 // only these kernels: config 4 at 8
@@ -347,6 +347,195 @@ __global__ __launch_bounds__(512) void k_gemv_lpr4m(const uint8_t* w, const uint
 hipError_t launch_gemv_lpr4m(dim3 groups, hipStream_t st, const LprArgs& a) {
   note_launch(reinterpret_cast<const void*>(&k_gemv_lpr4m));
   hipLaunchKernelGGL(k_gemv_lpr4m, groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G);
+  return hipGetLastError();
+}
+
+// 4-bit GI GEMV of 3..4 vectors with k_gemv_lpr's work layout and the
+// products on v_mfma_f32_4x4x4f16 (16 independent 4 x 4 x 4 blocks per
+// instruction).  Lane l owns row G g + l and wave w a contiguous eighth of
+// the row's chunks, as in k_gemv_lpr; the lookups are its bank-private pair
+// tables (entry b = LUT[b & 15] | LUT[b >> 4] << 16 at LDS dword 64 b + l),
+// so two lookups are the row's four consecutive k, exactly the A operand a
+// lane gives its 4 x 4 x 4 block (block l / 4, row l % 4).  The B operand of
+// lane l is x[l % 4][those four k] from LDS (x copied there once per
+// workgroup, as in k_gemv_lpr4m; vectors past nb read vector nb - 1, whose
+// output columns are never stored), and the block's result in lane l holds
+// rows 4 (l / 4) .. + 3 for vector l % 4.  Per 32 elements of a row: 16
+// lookups, 16 v_perm addresses, 4 16-byte x reads and 8 MFMAs, whatever the
+// vector count, where k_gemv_lpr issues 16 v_dot2 per vector and
+// k_gemv_lpr4m's 32 x 32 x 16 operands put both lanes of a row on one bank.
+// MI355X, 14336 x 4096, bench.py (graph-launched), the library with and
+// without it alternating on one box, three rounds: 3 / 4 vectors 8.04-8.21
+// / 8.10-8.25 us against 8.39-8.50 / 8.43-8.61 for k_gemv_lpr4m.  In one
+// process (both with this unit's max-ilp schedule): 2 vectors 7.78-8.02
+// against 7.91-8.09 for k_gemv_lpr (kept there), 1 and 8 vectors slower
+// (7.8-8.0 against 6.7-7.2, 10.3-10.6 against 9.2-9.5).  The eight waves' partials are added in wave
+// order.  Requires K % 256 == 0, G <= 64, 16-byte aligned x and
+// nb * (K / 2 + kLpr8mXPad) <= kLpr8mXDw; NCH > 0: the wave's chunk count
+// (K / 256) as a compile-time constant.
+template <int NCH>
+__device__ __forceinline__ void lpr4q_body(const LprArgs& a) {
+  constexpr int S = 8;
+  constexpr int LO = 16 / S;  // low nibbles of the table entries a wave builds
+  constexpr int R = NCH == 0 ? kLpr4qRing : (NCH < kLpr4qFirst ? NCH : kLpr4qFirst);
+  constexpr int DR = NCH == 0 ? kLpr4qRing : (R < kLpr4qAhead ? R : kLpr4qAhead);
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  // the table at LDS address 0 (a lookup needs no add), then x, then the
+  // waves' partials
+  __shared__ __attribute__((aligned(16))) uint32_t lds[kLprTableDw + kLpr8mXDw + S * 256];
+  uint32_t* const xs = lds + kLprTableDw;
+  float* const red = reinterpret_cast<float*>(xs + kLpr8mXDw);
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t N = a.N, K = a.K, G = a.G, nb = a.nb;
+  const uint32_t NC = K / 32, c0 = (w * NC) / S, nch = ((w + 1) * NC) / S - c0;
+  const uint32_t gbytes = gi_group_bytes(G, K, 4);
+  const uint32_t g = blockIdx.x;
+  const uint32_t gbase = g * gbytes;
+  const bool live = lane < G;
+  const __amdgpu_buffer_rsrc_t ri =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.w, (short)0, (int)(gridDim.x * gbytes), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)(nb * K * 2u), kBufferWord3);
+
+  // ---- loads in the order they are needed (they return in issue order):
+  // the LUT of row `lane`, x, the first chunks.  Lanes past G read zeros
+  // through the range check.
+  uint32_t L[8];
+  {
+    const uint32_t lo = live ? gbase + lane * 32u : 0x80000000u;
+    const u32x4v l0 = __builtin_amdgcn_raw_buffer_load_b128(ri, lo, 0u, 0);
+    const u32x4v l1 = __builtin_amdgcn_raw_buffer_load_b128(ri, lo + 16u, 0u, 0);
+    L[0] = l0.x; L[1] = l0.y; L[2] = l0.z; L[3] = l0.w;
+    L[4] = l1.x; L[5] = l1.y; L[6] = l1.z; L[7] = l1.w;
+  }
+  const uint32_t xq = nb * K / 8;  // 16-byte pieces of x (at most 4096: x <= 64 KB)
+  u32x4v xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t p = tid + 512u * i;
+    xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, p < xq ? p * 16u : 0x80000000u, 0u, 0);
+  }
+  const uint32_t cstride = G * kGiChunk;  // bytes from chunk c to c + 1 of a row
+  const uint32_t vbase = live ? gbase + G * 32u + (c0 * G + lane) * kGiChunk : 0x80000000u;
+  u32x4v ring[R];
+  auto ldc = [&](uint32_t i, u32x4v& dst) {
+    dst = __builtin_amdgcn_raw_buffer_load_b128(ri, i < nch ? vbase + i * cstride : 0x80000000u, 0u, kNontemporal);
+  };
+#pragma unroll
+  for (int u = 0; u < R; u++) ldc(u, ring[u]);
+
+  // ---- pair tables (wave w builds entries w + 8 i: low nibble w + 8 (i % 2)
+  // from the LUT registers with the wave-uniform w, high nibble i / 2) and x
+  uint32_t hv[LO];
+#pragma unroll
+  for (int j = 0; j < LO; j++) {
+    const uint32_t e = w + S * j;
+    uint32_t d = L[0];
+#pragma unroll
+    for (int q = 1; q < 8; q++) d = (e >> 1) == (uint32_t)q ? L[q] : d;
+    hv[j] = (e & 1) ? (d >> 16) : (d & 0xFFFFu);
+  }
+#pragma unroll
+  for (int i = 0; i < 256 / S; i++) {
+    const int hi = i / LO;
+    lds[(w + S * i) * 64 + lane] = __builtin_amdgcn_perm(L[hi >> 1], hv[i % LO], (hi & 1) ? 0x07060100u : 0x05040100u);
+  }
+  const uint32_t xrow = K / 2 + kLpr8mXPad;  // LDS dwords from one vector to the next
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t p = tid + 512u * i;
+    if (p < xq) {
+      const uint32_t b = p / (K / 8), o = p % (K / 8);
+      *reinterpret_cast<u32x4v*>(&xs[b * xrow + 4 * o]) = xv[i];
+    }
+  }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- lookups and products.  The B operand of lane l: vector l % 4 (nb - 1
+  // past nb), the wave's chunks from c0 on: 64 bytes of x per chunk.
+  const uint32_t lanebase = lane * 4u;
+  const uint32_t xv_lane = (lane & 3u) < nb ? (lane & 3u) : nb - 1;
+  const char* const xsb = reinterpret_cast<const char*>(xs) + (xv_lane * xrow * 4u + c0 * 64u);
+  f32x4 acc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  auto chunk = [&](uint32_t c, int slot, bool refill) {
+    uint32_t pr[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const uint32_t ad = __builtin_amdgcn_perm(ring[slot][j >> 2], lanebase, 0x0C0C0000u | ((4u + (j & 3)) << 8));
+      pr[j] = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lds) + ad);
+    }
+    if (refill) ldc(c + DR, ring[(slot + DR) % R]);
+    u32x4v xb[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) xb[m] = *reinterpret_cast<const u32x4v*>(xsb + c * 64u + 16u * m);
+    // step i: k 4 i .. 4 i + 3 of the chunk = the pairs of index bytes 2 i, 2 i + 1
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const u32x4v X = xb[i / 2];
+      const f16x4 A = __builtin_bit_cast(f16x4, u32x2v{pr[2 * i], pr[2 * i + 1]});
+      const f16x4 B = __builtin_bit_cast(f16x4, (i & 1) ? u32x2v{X.z, X.w} : u32x2v{X.x, X.y});
+      acc[i & 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(A, B, acc[i & 1], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (NCH > 0) {
+#pragma unroll
+    for (int c = 0; c < NCH; c++) chunk(c, c % R, c >= R - DR && c + DR < NCH);
+  } else {
+    // blocks of R chunks with the next block in flight; the last partial
+    // block skips its missing chunks (its requests read zeros)
+    uint32_t i = 0;
+    for (const uint32_t nfull = nch / R; i < nfull * R; i += R) {
+#pragma unroll
+      for (int u = 0; u < R; u++) chunk(i + u, u, true);
+    }
+#pragma unroll
+    for (int u = 0; u < R - 1; u++)
+      if (i + u < nch) chunk(i + u, u, true);
+  }
+
+  // ---- the eight waves' partials, added in wave order; lane l's result
+  // holds rows 4 (l / 4) .. + 3 of vector l % 4
+  *reinterpret_cast<f32x4*>(&red[(w * 64 + lane) * 4]) = acc[0] + acc[1];
+  __syncthreads();
+  for (uint32_t i = tid; i < 64u * nb; i += 512) {
+    const uint32_t v = i / 64, r = i % 64;
+    const uint32_t src = (4 * (r / 4) + v) * 4 + r % 4;
+    float sum = 0.0f;
+#pragma unroll
+    for (int v2 = 0; v2 < S; v2++) sum += red[v2 * 256 + src];
+    const uint32_t grow = g * G + r;
+    if (r < G && grow < N) a.y[(size_t)v * N + grow] = f2h(sum);
+  }
+}
+
+template <int NCH>
+__global__ __launch_bounds__(512) void k_gemv_lpr4q(const uint8_t* w, const uint8_t* w2, const uint16_t* x,
+                                                     uint16_t* y, uint16_t* y2, uint32_t N, uint32_t K, uint32_t nb,
+                                                     uint32_t G) {
+  lpr4q_body<NCH>(lpr_args(w, w2, x, y, y2, N, K, nb, G));
+}
+
+hipError_t launch_gemv_lpr4q(dim3 groups, hipStream_t st, const LprArgs& a) {
+  const uint32_t nch = a.K / 256;  // chunks per wave (K % 256 == 0)
+#define PRISM_LPR4Q(NCH_)                                                                                        \
+  do {                                                                                                           \
+    note_launch(reinterpret_cast<const void*>(&k_gemv_lpr4q<NCH_>));                                             \
+    hipLaunchKernelGGL(k_gemv_lpr4q<NCH_>, groups, dim3(512), 0, st, a.w, a.w2, a.x, a.y, a.y2, a.N, a.K, a.nb, a.G); \
+  } while (0)
+  if (nch == 16)
+    PRISM_LPR4Q(16);
+  else if (nch == 8)
+    PRISM_LPR4Q(8);
+  else
+    PRISM_LPR4Q(0);
+#undef PRISM_LPR4Q
   return hipGetLastError();
 }
 

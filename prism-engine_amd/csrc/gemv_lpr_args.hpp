@@ -49,6 +49,14 @@ constexpr int kLpr8mAhead = 4;
 constexpr int kLpr8mXPad = 4;       // dwords after each vector of x in LDS
 constexpr int kLpr8mXDw = 16512;  // LDS dwords for x: nb * (K / 2 + kLpr8mXPad) <= kLpr8mXDw
 
+// k_gemv_lpr4q (gemv_lpr8m.hip): chunk loads of a wave whose chunk count is
+// a compile-time constant, requested first and kept ahead of the lookups
+// (as k_gemv_lpr's kLprFirst / kLprAhead), and the run-time loop's ring
+// (blocks of kLpr4qRing chunks, the next block in flight).
+constexpr int kLpr4qFirst = 5;
+constexpr int kLpr4qAhead = 5;
+constexpr int kLpr4qRing = 4;
+
 // Records a launched kernel (by host function) in the launch log of the
 // compute call running on this thread, if any (prism_hip.hip).
 void note_launch(const void* fn);

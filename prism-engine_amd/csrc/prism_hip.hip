@@ -950,6 +950,21 @@ int launch_gemv_gi(prism_hip_ctx* ctx, const prism_hip_weight* w, const prism_hi
       a.K = K;
       a.nb = chunk = left;
       PRISM_LAUNCH((prism::k_gemv_generic<4, prism::kGenSingle, true>), dim3(N), dim3(64), 0, st, a);
+    } else if (!hg && G > 32 && (left == 3 || left == 4) && K % 256 == 0 &&
+               left * (K / 2 + prism::kLpr8mXPad) <= (uint32_t)prism::kLpr8mXDw) {
+      // 3..4 vectors over groups of 33..64 rows: k_gemv_lpr4q, the lane-per-row
+      // lookups feeding 4 x 4 x 4 matrix-core blocks.  MI355X, 14336 x 4096,
+      // bench.py alternating on one box: 3 / 4 vectors 8.04-8.21 /
+      // 8.10-8.25 us against 8.39-8.50 / 8.43-8.61 for k_gemv_lpr4m.
+      prism::LprArgs a{};
+      a.G = G;
+      a.w = w->d;
+      a.x = x;
+      a.y = y;
+      a.N = N;
+      a.K = K;
+      a.nb = chunk = left;
+      HIP_TRY(ctx, prism::launch_gemv_lpr4q(groups, st, a));
     } else if (!hg && G > 32 && left >= 3 && left <= 8 && K % 256 == 0 &&
                left * (K / 2 + prism::kLpr8mXPad) <= (uint32_t)prism::kLpr8mXDw) {
       // 3..8 vectors over groups of 33..64 rows (both row tiles of

@@ -476,3 +476,65 @@ def test_gemv_lpr4m_offsets(N, K, nb):
         perf = _check(np.where(p < xq, p * 16, 0x80000000), 0, 16, nb * K * 2, nb * K * 2, "gemv_lpr4m x")
         assert (perf == (p < xq)).all()
     assert ((tid[:, None] + 512 * np.arange(8)[None, :]) < xq).sum() == xq, "x pieces cover x once"
+
+
+LPR4Q_AHEAD = _const("gemv_lpr_args.hpp", "kLpr4qAhead")
+LPR4Q_RING = _const("gemv_lpr_args.hpp", "kLpr4qRing")
+
+
+@pytest.mark.parametrize("N,K,nb", [(14336, 4096, 4), (14336, 4096, 3), (9100, 2048, 4), (14336, 8192, 4),
+                                    (9000, 2304, 3), (12000, 3328, 4)])
+def test_gemv_lpr4q_offsets(N, K, nb):
+    """k_gemv_lpr4q (gemv_lpr8m.hip): the LUT of row `lane` (two 16-byte
+    loads, lanes past G an offset past the range); x in 16-byte pieces; chunk
+    c0 + i of row `lane`, or an offset past the range from the wave's chunk
+    count on (the compile-time sequence requests up to kLpr4qAhead past it,
+    the run-time loop a block of kLpr4qRing); each lane's LDS x reads stay
+    inside its vector and hold the k its A operand holds."""
+    G = gi_rows(N, K)
+    xrow = K // 2 + LPR8M_XPAD
+    assert G > 32 and K % 256 == 0 and nb in (3, 4) and nb * xrow <= LPR8M_XDW, "the host's condition"
+    S = 8
+    nc = K // 32
+    nch = nc // S
+    compile_time = nch in (8, 16)
+    ahead = LPR4Q_AHEAD if compile_time else LPR4Q_RING
+    lane = np.arange(64)
+    ngroups = -(-N // G)
+    gb = gi_group_bytes(G, K)
+    nbytes = ngroups * gb
+    for g in (0, ngroups - 1):
+        base = g * gb
+        lo = np.where(lane < G, base + lane * 32, 0x80000000)
+        for i in range(2):
+            perf = _check(lo + 16 * i, 0, 16, nbytes, nbytes, "gemv_lpr4q LUT")
+            assert (perf == (lane < G)).all()
+            assert ((lo + 16 * i + 16) <= base + G * 32)[perf].all(), "LUT load leaves the group's LUTs"
+        for w in range(S):
+            c0 = (w * nc) // S
+            assert ((w + 1) * nc) // S - c0 == nch
+            vbase = np.where(lane < G, base + G * 32 + (c0 * G + lane) * GI_CHUNK, 0x80000000)
+            for i in range(nch + ahead):  # every chunk request, the ones past the range included
+                vo = vbase + i * G * GI_CHUNK if i < nch else np.full(64, 0x80000000)
+                perf = _check(vo, 0, 16, nbytes, nbytes, "gemv_lpr4q chunk")
+                assert (perf == ((lane < G) & (i < nch))).all()
+                assert ((vo + 16) <= base + gb)[perf].all(), "chunk load leaves its group"
+            # LDS x reads of lane l: vector min(l % 4, nb - 1), bytes 64 (c0 + c) + 16 m, m < 4
+            vec = np.minimum(lane % 4, nb - 1)
+            for c in (0, nch - 1):
+                for m in range(4):
+                    off = vec * xrow * 4 + (c0 + c) * 64 + 16 * m
+                    assert ((off + 16) <= vec * xrow * 4 + K * 2).all(), "x read leaves its vector"
+                    for half in range(2):  # MFMA step 2 m + half: x elements and weight elements agree
+                        step = 2 * m + half
+                        xel = (off + 8 * half - vec * xrow * 4) // 2
+                        assert (xel == 32 * (c0 + c) + 4 * step).all()
+    tid = np.arange(512)
+    xq = nb * K // 8
+    for i in range(8):
+        p = tid + 512 * i
+        perf = _check(np.where(p < xq, p * 16, 0x80000000), 0, 16, nb * K * 2, nb * K * 2, "gemv_lpr4q x")
+        assert (perf == (p < xq)).all()
+        b, o = p // (K // 8), p % (K // 8)
+        assert ((b * xrow + 4 * o + 4) <= LPR8M_XDW)[p < xq].all(), "x store leaves its LDS region"
+    assert ((tid[:, None] + 512 * np.arange(8)[None, :]) < xq).sum() == xq, "x pieces cover x once"

@@ -349,8 +349,8 @@ def test_gi4_decode_bit_exact_through_lpr(pe, gpu_ctx, N, K):
 @pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048)])
 def test_gi4_decode_bit_exact_through_lpr4m(pe, gpu_ctx, N, K):
     """One-hot x, a different column per vector, through the 4-bit
-    lane-per-row lookups feeding the matrix cores (k_gemv_lpr4m, 3 and 8
-    vectors): every output is LUT_r[idx(r, k)] exactly.  The columns cover
+    lane-per-row lookups feeding the matrix cores (k_gemv_lpr4q at 3
+    vectors, k_gemv_lpr4m at 8): every output is LUT_r[idx(r, k)] exactly.  The columns cover
     both lanes of a row (chunks 2s and 2s + 1), every MFMA of a step (index
     dwords 0..3 of a chunk), the K quarters' edges and the row's end."""
     t = pe.synth_tensor(N, K, 4, seed=K + 41)
@@ -369,7 +369,7 @@ def test_gi4_decode_bit_exact_through_lpr4m(pe, gpu_ctx, N, K):
             for v, k in enumerate(cols):
                 x[v, k] = 1.0
             y = gpu_ctx.gemv(w, x.view(np.uint16))
-            assert gpu_ctx.last_kernels() == "k_gemv_lpr4m"
+            assert gpu_ctx.last_kernels() == ("k_gemv_lpr4m" if len(cols) > 4 else f"k_gemv_lpr4q<{K // 256}>")
             for v, k in enumerate(cols):
                 want = lut[rows, idx[:, k]]
                 want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
@@ -378,11 +378,43 @@ def test_gi4_decode_bit_exact_through_lpr4m(pe, gpu_ctx, N, K):
     w.free()
 
 
-@pytest.mark.parametrize("batch,kernel", [(3, "k_gemv_lpr4m"), (4, "k_gemv_lpr4m"), (5, "k_gemv_mfma<4, true>")])
+@pytest.mark.parametrize("N,K", [(14336, 4096), (9100, 2048), (12000, 3328)])
+def test_gi4_decode_bit_exact_through_lpr4q(pe, gpu_ctx, N, K):
+    """One-hot x through k_gemv_lpr4q at 4 vectors (every block column
+    live), a different column per vector: every element of the first wave's
+    first chunk (all eight 4 x 4 x 4 steps, both halves of each step's A
+    operand), then the first element of every chunk of a wave's range, the
+    waves' edges and the row's end.  The one nonzero product is added to
+    zeros, so each output is LUT_r[idx(r, k)] exactly."""
+    t = pe.synth_tensor(N, K, 4, seed=K + 43)
+    lut, idx = pe.unpack_payload(t.payload, N, K, 4)
+    wk = K // 8  # elements of a wave's range
+    ks = list(range(32)) + [32 * c for c in range(1, wk // 32)] + [wk - 1, wk, 3 * wk + 5, K - 33, K - 32, K - 2, K - 1]
+    ks += [ks[-1]] * (-len(ks) % 4)
+    w = gpu_ctx.upload_tensor(t)
+    print(f"gi4 one-hot lpr4q {N}x{K}", flush=True)
+    rows = np.arange(N)
+    want_kernel = f"k_gemv_lpr4q<{K // 256 if K // 256 in (8, 16) else 0}>"
+    for c0 in range(0, len(ks), 4):
+        cols = ks[c0:c0 + 4]
+        x = np.zeros((4, K), dtype=np.float16)
+        for v, k in enumerate(cols):
+            x[v, k] = 1.0
+        y = gpu_ctx.gemv(w, x.view(np.uint16))
+        assert gpu_ctx.last_kernels() == want_kernel
+        for v, k in enumerate(cols):
+            want = lut[rows, idx[:, k]]
+            want = np.where(want == 0x8000, 0, want)  # 0.0 + (-0.0) = +0.0
+            bad = np.nonzero(y[v] != want)[0]
+            assert bad.size == 0, f"column {k}: {bad.size} rows differ (first {bad[:4]})"
+    w.free()
+
+
+@pytest.mark.parametrize("batch,kernel", [(3, "k_gemv_lpr4q<0>"), (4, "k_gemv_lpr4q<0>"), (5, "k_gemv_mfma<4, true>")])
 def test_gi4_k8192_lpr4m_edge(pe, oracle, gpu_ctx, batch, kernel):
-    """4-bit GI rows of 8192 (32 double steps per wave): 3 and 4 vectors of
-    x (4 x 4100 dwords) fit k_gemv_lpr4m's LDS, 5 do not and take the
-    matrix-core GEMV; against the oracle."""
+    """4-bit GI rows of 8192: 3 and 4 vectors of x (4 x 4100 dwords) fit the
+    LDS of k_gemv_lpr4q (32 chunks per wave: its run-time loop), 5 do not
+    and take the matrix-core GEMV; against the oracle."""
     N, K = 14336, 8192
     assert _gi(N, K) == 56
     t = pe.synth_tensor(N, K, 4, seed=K + batch + 4)
@@ -395,18 +427,21 @@ def test_gi4_k8192_lpr4m_edge(pe, oracle, gpu_ctx, batch, kernel):
     w.free()
 
 
-@pytest.mark.parametrize("N,K,batch", [(9000, 2304, 5), (12000, 3328, 7), (16384, 2048, 4)])
-def test_gi4_lpr4m_row_lengths(pe, oracle, gpu_ctx, N, K, batch):
+@pytest.mark.parametrize("N,K,batch,kernel", [(9000, 2304, 5, "k_gemv_lpr4m"), (12000, 3328, 7, "k_gemv_lpr4m"),
+                                              (16384, 2048, 4, "k_gemv_lpr4q<8>"), (9000, 2304, 3, "k_gemv_lpr4q<0>"),
+                                              (12000, 3328, 4, "k_gemv_lpr4q<0>"), (16384, 2048, 6, "k_gemv_lpr4m")])
+def test_gi4_lpr4m_row_lengths(pe, oracle, gpu_ctx, N, K, batch, kernel):
     """k_gemv_lpr4m where a wave's double steps are not a multiple of the
     four in flight (K = 2304: 9 per wave; 3328: 13), and over 64-row groups;
-    against the oracle."""
+    k_gemv_lpr4q where a wave's chunks are not a multiple of its run-time
+    loop's blocks of four (9, 13); against the oracle."""
     assert _gi(N, K) > 32
     t = pe.synth_tensor(N, K, 4, seed=N + K + batch)
     x = pe.synth_x(batch, K, seed=batch + 61)
     w = gpu_ctx.upload_tensor(t)
-    print(f"gi4 lpr4m {N}x{K} batch {batch}", flush=True)
+    print(f"gi4 {kernel} {N}x{K} batch {batch}", flush=True)
     y = gpu_ctx.gemv(w, x)
-    assert gpu_ctx.last_kernels() == "k_gemv_lpr4m"
+    assert gpu_ctx.last_kernels() == kernel
     _check(y, oracle.gemv(x, t.payload, N, K, 4, threads=8), f"GI4 {N}x{K} batch {batch}")
     w.free()
 
