@@ -137,6 +137,14 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   const uint32_t N = a.N, K = a.K, NC = K / 32;
   const uint32_t G = a.G;
   const uint32_t c0 = (w * NC) / S, nch = ((w + 1) * NC) / S - c0;
+  // The half-group form with NCH > 0 (launched only when every wave has NCH
+  // chunks) takes the count as a compile-time constant, so the ring's and
+  // the x blocks' range checks fold (the run-time count costs each refill a
+  // compare and selects): config 2 13.56-13.61 against 13.65-13.71 us, three
+  // alternating rounds on one box.  The one-group form keeps the run-time
+  // count: with the constant the hero took 6.82-6.85 against 6.40-6.45 us in
+  // the same rounds (its schedule moved), config 4's 8-bit form no faster.
+  const uint32_t nchk = (HG && NCH > 0) ? (uint32_t)NCH : nch;
   const uint32_t gbytes = G * 32u + G * (K / 2);
   const uint32_t nbytes = ((N + G - 1) / G) * gbytes;
   // the lane's group, its row in the group and the group's byte offset
@@ -211,7 +219,7 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
   const uint32_t vbase = live ? gbase + G * 32u + (c0 * G + lr) * kGiChunk : 0x80000000u;
   u32x4v ring[R][NT];
   auto ldc = [&](uint32_t i, u32x4v (&dst)[NT]) {
-    const uint32_t vo = i < nch ? vbase + i * cstride : SPLIT ? vbase : 0x80000000u;
+    const uint32_t vo = i < nchk ? vbase + i * cstride : SPLIT ? vbase : 0x80000000u;
 #pragma unroll
     for (int m = 0; m < NT; m++) dst[m] = ld_idx(m, vo);
   };
@@ -230,7 +238,7 @@ __device__ __forceinline__ void lpr_body(const LprArgs& a) {
     for (int b = 0; b < NB; b++)
 #pragma unroll
       for (int u = 0; u < XB; u++)
-        xs[b][u] = xw[((uint32_t)b < a.nb ? (uint32_t)b : 0u) * xrow + (i + u < nch ? i + u : 0)];
+        xs[b][u] = xw[((uint32_t)b < a.nb ? (uint32_t)b : 0u) * xrow + (i + u < nchk ? i + u : 0)];
   };
   ldx(0);
 
