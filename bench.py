@@ -68,6 +68,8 @@ WORKLOADS = {
     "cfg1": ("gemv", 4, 4864, 896, 1),
     "cfg2": ("gateup", 4, 18944, 3584, 1),
     "cfg4": ("gemv", 8, 14336, 4096, 1),
+    # config 2's gate matrix alone (74 rows per CU: the half-group GI layout), for batch sweeps
+    "hgmat": ("gemv", 4, 18944, 3584, 1),
     "cfg5": ("gemm", 4, 14336, 4096, 2048),
     "gemm8": ("gemm", 8, 14336, 4096, 2048),  # the cfg5 shape with 8-bit weights (not a BASELINE config)
     "cfg3": ("decode", 4, 0, 0, 1),
