@@ -85,6 +85,8 @@ WORKLOADS = {
     # measuring sticks: one dependent launch, the matrix cores' rate
     "launch": ("launch", 0, 0, 0, 1),
     "mfma": ("mfma", 0, 0, 0, 1),
+    # instruction issue rates (v_fma_f32, v_dot2_f32_f16, v_perm_b32, v_mfma_f32_4x4x4f16) at 1 / 2 / 4 waves per SIMD
+    "issue": ("issue", 0, 0, 0, 1),
 }
 PCIE_PEAK_GBS = 63.0  # PCIe 5.0 x16, one direction
 DECODE_KV_LEN = 512
@@ -677,12 +679,39 @@ def run_probe(args, pe, kind: str) -> int:
     mfma: register-only matrix-core work, every CU (num_cu workgroups of one
     wave per SIMD) and three quarters of them, timed the same way as the
     GEMV workloads (value: TFLOP/s over all CUs; the line also carries the
-    rate per CU at 3/4 of them)."""
+    rate per CU at 3/4 of them).  issue: the issue rate of four instruction
+    kinds (v_fma_f32, v_dot2_f32_f16, v_perm_b32, v_mfma_f32_4x4x4f16) with 1,
+    2 and 4 waves per SIMD on every CU, in ns per instruction per SIMD
+    (value: v_mfma_f32_4x4x4f16 at 2 waves per SIMD, the lane-per-row GEMVs'
+    occupancy; the line carries the whole table)."""
     import torch
     ctx = pe.Context(0)
     dev = torch.device("cuda", 0)
     stream = torch.cuda.Stream(device=dev)
     ncu = torch.cuda.get_device_properties(dev).multi_processor_count
+    if kind == "issue":
+        sink = torch.zeros(256, dtype=torch.float32, device=dev)
+        iters = 2000
+        names = ["v_fma_f32", "v_dot2_f32_f16", "v_perm_b32", "v_mfma_f32_4x4x4f16"]
+        table = {}
+        for op, name in enumerate(names):
+            for wps in (1, 2, 4):
+                def launch(i: int, o=op, w=wps) -> None:
+                    ctx.issue_probe_dev(o, ncu, w, iters, sink, stream)
+                ms, _, mode = time_launches(launch, args.steps, args.warmup, stream, not args.no_graph)
+                ns = ms / args.steps * 1e6 / (iters * 8 * wps)  # per instruction per SIMD
+                table.setdefault(name, {})[f"{wps}_waves_per_simd"] = round(ns, 3)
+                log(f"[bench] {name}, {wps} wave(s) per SIMD: {ns:.3f} ns per instruction per SIMD ({mode})")
+        v = table["v_mfma_f32_4x4x4f16"]["2_waves_per_simd"]
+        rec = {"metric": "ns per v_mfma_f32_4x4x4f16 per SIMD (2 waves per SIMD, every CU)", "value": v,
+               "unit": "ns", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "ms_per_step": None, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+               "dtype": "fp32 / fp16 register operands", "data": "synthetic register operands",
+               "config": {"workload": "issue", "kind": "probe", "workgroups": ncu, "rounds": iters,
+                          "chains_per_wave": 8},
+               "issue_ns_per_instruction_per_simd": table, "roofline": None, "cpu_baseline": None}
+        print(json.dumps(rec), flush=True)
+        return 0
     if kind == "launch":
         def launch(i: int) -> None:
             ctx.launch_empty_dev(stream)
@@ -774,7 +803,7 @@ def main() -> int:
         return run_palettize(args, pe, pe.SEEDS.get(args.workload, 1006))
     if kind == "load":
         return run_load(args, pe, pe.SEEDS.get(args.workload, 1007))
-    if kind in ("launch", "mfma"):
+    if kind in ("launch", "mfma", "issue"):
         return run_probe(args, pe, kind)
     if args.batch is not None and kind in ("gemv", "gemm"):
         batch = args.batch  # batch vectors, or the GEMM's rows of X

@@ -316,6 +316,15 @@ int prism_hip_stream_read_dev(prism_hip_ctx* ctx, const void* d_buf, size_t byte
 int prism_hip_launch_empty_dev(prism_hip_ctx* ctx, void* stream);
 int prism_hip_mfma_probe_dev(prism_hip_ctx* ctx, uint32_t groups, uint32_t iters, void* d_sink, void* stream);
 
+/* Issue-rate probe, no counterpart in the reference: `groups` workgroups of
+ * 256 * waves_per_simd threads (1, 2 or 4 waves on each SIMD), each wave
+ * running `iters` rounds of 8 independent instructions of kind `op`: 0
+ * v_fma_f32, 1 v_dot2_f32_f16, 2 v_perm_b32, 3 v_mfma_f32_4x4x4f16.  d_sink
+ * (>= 1 KB of device memory) is (almost surely) not written.  Enqueues on
+ * `stream` (NULL: the context stream) and returns. */
+int prism_hip_issue_probe_dev(prism_hip_ctx* ctx, uint32_t op, uint32_t groups, uint32_t waves_per_simd,
+                              uint32_t iters, void* d_sink, void* stream);
+
 /* The kernels the dispatch launched in the context's most recent compute
  * call (GEMV, gate/up, GEMM, row decode, palettize, read floor), by their
  * device names in launch order, joined by " + ", e.g.

@@ -115,6 +115,9 @@ extern "C" {
     pub fn prism_hip_launch_empty_dev(ctx: *mut prism_hip_ctx, stream: *mut c_void) -> c_int;
     pub fn prism_hip_mfma_probe_dev(ctx: *mut prism_hip_ctx, groups: u32, iters: u32, d_sink: *mut c_void,
         stream: *mut c_void) -> c_int;
+    // No reference counterpart: one instruction kind's issue rate
+    pub fn prism_hip_issue_probe_dev(ctx: *mut prism_hip_ctx, op: u32, groups: u32, waves_per_simd: u32,
+        iters: u32, d_sink: *mut c_void, stream: *mut c_void) -> c_int;
     // No reference counterpart: the kernels the last compute call launched
     pub fn prism_hip_last_kernels(ctx: *mut prism_hip_ctx) -> *const c_char;
 }

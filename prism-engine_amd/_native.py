@@ -103,6 +103,7 @@ SIGNATURES = {
     "prism_hip_stream_read_dev": (_c.c_int, [_vp, _vp, _c.c_size_t, _vp, _vp]),
     "prism_hip_launch_empty_dev": (_c.c_int, [_vp, _vp]),
     "prism_hip_mfma_probe_dev": (_c.c_int, [_vp, _c.c_uint32, _c.c_uint32, _vp, _vp]),
+    "prism_hip_issue_probe_dev": (_c.c_int, [_vp, _c.c_uint32, _c.c_uint32, _c.c_uint32, _c.c_uint32, _vp, _vp]),
     "prism_hip_last_kernels": (_c.c_char_p, [_vp]),
 }
 

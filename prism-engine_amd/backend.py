@@ -164,6 +164,12 @@ class Context:
         """`groups` workgroups of register-only MFMA rounds (measure_kernels.hpp)."""
         self.check(self.lib.prism_hip_mfma_probe_dev(self.h, groups, iters, ptr(d_sink), _stream_handle(stream)))
 
+    def issue_probe_dev(self, op: int, groups: int, waves_per_simd: int, iters: int, d_sink, stream=None) -> None:
+        """Issue-rate probe (measure_kernels.hpp k_issue_probe): op 0 v_fma_f32,
+        1 v_dot2_f32_f16, 2 v_perm_b32, 3 v_mfma_f32_4x4x4f16."""
+        self.check(self.lib.prism_hip_issue_probe_dev(self.h, op, groups, waves_per_simd, iters, ptr(d_sink),
+                                                      _stream_handle(stream)))
+
     def gemm_dev(self, w: "Weight", d_X, M: int, d_Y, stream=None) -> None:
         self.check(self.lib.prism_hip_gemm_dev(self.h, w.h, ptr(d_X), M, ptr(d_Y), _stream_handle(stream)))
 

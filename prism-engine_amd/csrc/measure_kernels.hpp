@@ -87,4 +87,79 @@ __global__ __launch_bounds__(256) void k_mfma_probe(uint32_t iters, float* __res
   if (s == 1234.5f) sink[threadIdx.x & 255u] = s;
 }
 
+// Issue rate of one instruction kind (bench.py --workload issue): each wave
+// runs `iters` rounds of 8 independent instructions of kind OP (0
+// v_fma_f32, 1 v_dot2_f32_f16, 2 v_perm_b32, 3 v_mfma_f32_4x4x4f16, whose 16
+// blocks are the lane-per-row GEMV's A operands in k_gemv_lpr4q); the
+// workgroup's size sets the waves per SIMD.  The result is written only if
+// it equals a constant.  It shows how many cycles apart one wave issues
+// VALU instructions, how the SIMD's rate grows with more waves, and what a
+// 4 x 4 x 4 matrix-core instruction costs beside the v_dot2 it replaces.
+template <int OP>
+__global__ __launch_bounds__(1024) void k_issue_probe(uint32_t iters, float* __restrict__ sink) {
+  typedef _Float16 h2p __attribute__((ext_vector_type(2)));
+  typedef _Float16 h4p __attribute__((ext_vector_type(4)));
+  typedef float f4p __attribute__((ext_vector_type(4)));
+  const uint32_t t = threadIdx.x;
+  float s = 0.0f;
+  if constexpr (OP == 0) {
+    float a[8];
+    float b = 1.0001f + (float)t * 1e-7f;
+    for (int j = 0; j < 8; j++) a[j] = 0.5f + (float)(j + t);
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[j] = __builtin_fmaf(a[j], b, 0.25f);
+      b = b * 0.99999f;
+    }
+    for (int j = 0; j < 8; j++) s += a[j];
+  } else if constexpr (OP == 1) {
+    uint32_t a[8];
+    uint32_t b = 0x3c003c00u ^ t;
+    float c[8];
+    for (int j = 0; j < 8; j++) {
+      a[j] = 0x3c003c00u + (uint32_t)j * 0x00010001u + t;
+      c[j] = 0.0f;
+    }
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        c[j] = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2p, a[j]), __builtin_bit_cast(h2p, b), c[j], false);
+      b = (b << 1) | (b >> 31);
+    }
+    for (int j = 0; j < 8; j++) s += c[j];
+  } else if constexpr (OP == 2) {
+    uint32_t a[8];
+    uint32_t b = 0x01020304u ^ t;
+    for (int j = 0; j < 8; j++) a[j] = 0x3c003c00u + (uint32_t)j * 0x00010001u + t;
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[j] = __builtin_amdgcn_perm(a[j], b, 0x05040100u + (uint32_t)j);
+      b += 0x01010101u;
+    }
+    uint32_t x = 0;
+    for (int j = 0; j < 8; j++) x ^= a[j];
+    // an integer test: a float compare that can never hold would let the
+    // compiler drop the loop
+    if (x == 0x9E3779B9u) sink[t & 255u] = 1.0f;
+    return;
+  } else {
+    h4p a[8], b;
+    f4p c[8];
+    for (int j = 0; j < 8; j++)
+      for (int i = 0; i < 4; i++) a[j][i] = (_Float16)(0.001f * (float)(t + j + i));
+    for (int i = 0; i < 4; i++) b[i] = (_Float16)(0.5f + 0.01f * (float)i);
+    for (int j = 0; j < 8; j++) c[j] = f4p{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t it = 0; it < iters; it++) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) c[j] = __builtin_amdgcn_mfma_f32_4x4x4f16(a[j], b, c[j], 0, 0, 0);
+      b = h4p{b.y, b.z, b.w, b.x};
+    }
+    for (int j = 0; j < 8; j++) {
+      const float v = c[j][0];
+      s += v;
+    }
+  }
+  if (s == 1234.5f) sink[t & 255u] = s;
+}
+
 }  // namespace prism

@@ -1678,6 +1678,30 @@ int prism_hip_mfma_probe_dev(prism_hip_ctx* ctx, uint32_t groups, uint32_t iters
   return PRISM_HIP_OK;
 }
 
+int prism_hip_issue_probe_dev(prism_hip_ctx* ctx, uint32_t op, uint32_t groups, uint32_t waves_per_simd,
+                              uint32_t iters, void* d_sink, void* stream) {
+  if (!ctx) return PRISM_HIP_ERR_NULL;
+  if (!d_sink) return fail(ctx, PRISM_HIP_ERR_NULL, "sink is NULL");
+  if (op > 3) return fail(ctx, PRISM_HIP_ERR_SHAPE, "instruction kind %u: 0..3", op);
+  if (waves_per_simd != 1 && waves_per_simd != 2 && waves_per_simd != 4)
+    return fail(ctx, PRISM_HIP_ERR_SHAPE, "%u waves per SIMD: 1, 2 or 4", waves_per_simd);
+  if (groups == 0 || groups > 65536) return fail(ctx, PRISM_HIP_ERR_SIZE, "%u workgroups: 1..65536", groups);
+  DeviceGuard g(ctx->device);
+  LaunchLog log(ctx);
+  const dim3 block(256 * waves_per_simd);
+  hipStream_t st = pick_stream(ctx, stream);
+  float* sink = reinterpret_cast<float*>(d_sink);
+  switch (op) {
+    case 0: PRISM_LAUNCH(prism::k_issue_probe<0>, dim3(groups), block, 0, st, iters, sink); break;
+    case 1: PRISM_LAUNCH(prism::k_issue_probe<1>, dim3(groups), block, 0, st, iters, sink); break;
+    case 2: PRISM_LAUNCH(prism::k_issue_probe<2>, dim3(groups), block, 0, st, iters, sink); break;
+    default: PRISM_LAUNCH(prism::k_issue_probe<3>, dim3(groups), block, 0, st, iters, sink); break;
+  }
+  HIP_TRY(ctx, hipGetLastError());
+  ctx->err.clear();
+  return PRISM_HIP_OK;
+}
+
 }  // extern "C"
 
 // GPU-resident decode step (prism_hip_model_*).
